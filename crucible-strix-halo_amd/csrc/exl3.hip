@@ -1,0 +1,295 @@
+// EXL3 linear op on MI355X: loader repack, bit-exact dequant, and the linear
+// (input transform -> fused decode/MFMA GEMM -> fixed-order split sum + output transform).
+#include "internal.hpp"
+
+namespace cx {
+
+// ---- loader repack ------------------------------------------------------------------
+
+// Checkpoint tile (a, b) -> column-pair-major index ((b/2) A + a) 2 + b % 2.  The 8K
+// dwords of a tile are its 16K little-endian int16 words unchanged.
+__global__ void RepackKernel(const uint32_t* __restrict__ src, uint32_t* __restrict__ dst, int A, int B, int T) {
+  const size_t total = (size_t)A * B * T;
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+    const size_t tile = i / T;
+    const int w = (int)(i % T);
+    const int a = (int)(tile / B), b = (int)(tile % B);
+    const size_t d = (((size_t)(b >> 1) * A + a) * 2 + (b & 1)) * T + w;
+    dst[d] = src[i];
+  }
+}
+
+// ---- dequant ------------------------------------------------------------------------
+
+// One wave per tile pair: the GEMM's own decode (same lanes, same arithmetic), written
+// out as W_hat[16a + r][16b + c].
+template <int K2, int CB>
+__global__ void __launch_bounds__(256) DequantKernel(const uint32_t* __restrict__ tiles, __half* __restrict__ w,
+                                                     int A, int ncp) {
+  constexpr int T = TileDwords(K2);
+  constexpr int ND = WindowDwords(K2);
+  const int pair = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (pair >= A * ncp) return;
+  const int lane = threadIdx.x & 63;
+  const int cp = pair / A, a = pair % A;
+  const uint32_t* base = tiles + (size_t)pair * 2 * T;
+  const LaneRun<K2> lr(lane);
+  uint32_t win[3] = {0, 0, 0};
+#pragma unroll
+  for (int i = 0; i < ND; ++i) win[i] = base[lr.ByteOffset(i) / 4];
+  half4_t lo, hi;
+  DecodeRun<K2, CB>(win[0], win[1], ND > 2 ? win[2] : win[1], lr.shift, lo, hi);
+  const int O = ncp * 32;
+  const int q = lane >> 4, c = (lane & 7), b = 2 * cp + ((lane & 15) >> 3);
+  // (Elements go through scalar locals: bit-casting a vector element lvalue directly
+  // is miscompiled by this toolchain into element 0 for every index.)
+  unsigned short* wu = reinterpret_cast<unsigned short*>(w);
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const int r = 16 * a + PermRow16(4 * q + s);
+    const _Float16 vlo = lo[s], vhi = hi[s];
+    wu[(size_t)r * O + b * 16 + c] = __builtin_bit_cast(unsigned short, vlo);
+    wu[(size_t)r * O + b * 16 + c + 8] = __builtin_bit_cast(unsigned short, vhi);
+  }
+}
+
+// ---- activation transforms ----------------------------------------------------------
+
+// Input transform of fp16 rows: RoundH(x * suh) -> WHT128 -> * norm -> fp16, stored in
+// MFMA row order.  One 128-block per 32 lanes.  rows[i] (nullable) maps output row i to
+// its input row.  ref/exl3_ref.py:140-152; engine/exl3/exl3.h:48-65.
+__global__ void __launch_bounds__(256) InputTransformKernel(const __half* __restrict__ x, int ldx,
+                                                            const int* __restrict__ rows, const __half* __restrict__ suh,
+                                                            __half* __restrict__ xp, int M, int I) {
+  const int nb = I / 128;
+  const int item = (blockIdx.x * blockDim.x + threadIdx.x) >> 5;
+  if (item >= M * nb) return;
+  const int r = item / nb, blk = item % nb, j = threadIdx.x & 31;
+  const int src = rows ? rows[r] : r;
+  const int c0 = blk * 128 + 4 * j;
+  const __half* xr = x + (size_t)src * ldx + c0;
+  float v[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = RoundH(H2F(xr[i]) * H2F(suh[c0 + i]));
+  Wht128x4(v);
+  __half* d = xp + (size_t)r * I + blk * 128;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int e = 4 * j + i;
+    d[(e & ~15) + PermPos16(e & 15)] = __float2half(v[i] * kHadNorm);
+  }
+}
+
+// Fixed-order sum of S K-segment partials, then the output transform.
+// f16 = 0: WHT in fp32, * (norm * svh) (engine LinOutBlock, engine/exl3/exl3.h:69-82).
+// f16 = 1: y_h rounded to fp16, WHT, * norm -> fp16, * svh -> fp16 (ref/exl3_ref.py:153-156).
+__global__ void __launch_bounds__(256) OutputTransformKernel(const float* __restrict__ part, long long seg_stride,
+                                                             int S, const __half* __restrict__ svh, void* y, int M,
+                                                             int O, int f16) {
+  const int nb = O / 128;
+  const int item = (blockIdx.x * blockDim.x + threadIdx.x) >> 5;
+  if (item >= M * nb) return;
+  const int r = item / nb, blk = item % nb, j = threadIdx.x & 31;
+  const int c0 = blk * 128 + 4 * j;
+  float v[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < S; ++s) {
+    const float4 p = *reinterpret_cast<const float4*>(part + s * seg_stride + (size_t)r * O + c0);
+    v[0] += p.x;
+    v[1] += p.y;
+    v[2] += p.z;
+    v[3] += p.w;
+  }
+  if (f16) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = RoundH(v[i]);
+  }
+  Wht128x4(v);
+  if (f16) {
+    __half* d = reinterpret_cast<__half*>(y) + (size_t)r * O + c0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) d[i] = __float2half(RoundH(v[i] * kHadNorm) * H2F(svh[c0 + i]));
+  } else {
+    float* d = reinterpret_cast<float*>(y) + (size_t)r * O + c0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) d[i] = v[i] * (kHadNorm * H2F(svh[c0 + i]));
+  }
+}
+
+// ---- host side ------------------------------------------------------------------------
+
+int CheckMatrix(const cx_exl3_matrix* m) {
+  if (!m || !m->tiles || !m->suh || !m->svh) return CX_E_ARG;
+  if (m->in_features <= 0 || m->out_features <= 0 || m->in_features % 128 || m->out_features % 128) return CX_E_SHAPE;
+  if (!ValidK2(m->k2)) return CX_E_BITRATE;
+  if (m->codebook < 0 || m->codebook > 2) return CX_E_ARG;
+  if ((m->k2 & 1) && m->codebook != CX_CB_MUL1) return CX_E_BITRATE;  // half rates require mul1
+  return CX_OK;
+}
+
+int RowOffsetsCheck(const int32_t* row_offsets, int32_t n_sessions, int32_t M) {
+  if (!row_offsets) return CX_OK;
+  if (n_sessions < 1 || row_offsets[0] != 0) return CX_E_SHAPE;
+  for (int s = 0; s < n_sessions; ++s)
+    if (row_offsets[s + 1] < row_offsets[s]) return CX_E_SHAPE;
+  return row_offsets[n_sessions] == M ? CX_OK : CX_E_SHAPE;
+}
+
+LinearPlan PlanLinear(int I, int O, int M) {
+  LinearPlan p;
+  p.A = I / 16;
+  p.ncp = O / 32;
+  p.nrb = M >= 64 ? 4 : (M + 15) / 16;
+  if (p.nrb < 1) p.nrb = 1;
+  p.chunk = 16 * p.nrb;
+  p.n_entries = (M + p.chunk - 1) / p.chunk;
+  p.ksw = 4;
+  // Grow the cross-workgroup K split until ~512 workgroups or 4 steps per wave.  The
+  // split depends on the matrix only, never on M, so a row's result is bitwise the same
+  // whatever other rows share the call.
+  p.S = 1;
+  const int wgs = p.ncp;
+  while (wgs * p.S < 512 && p.A % (p.ksw * p.S * 2) == 0 && p.A / (p.ksw * p.S * 2) >= 4) p.S *= 2;
+  const int steps = p.A / (p.ksw * p.S);
+  p.u = steps % 4 == 0 ? 4 : steps % 2 == 0 ? 2 : 1;
+  return p;
+}
+
+__global__ void FillLinearTablesKernel(int4* ent, MatPtr* mat, int first, int n_entries, int chunk, int M, MatPtr m) {
+  const int i = threadIdx.x, e = first + i;
+  if (i < n_entries) ent[i] = make_int4(0, e * chunk, min(chunk, M - e * chunk), 0);
+  if (i == 0) mat[0] = m;
+}
+
+void FillLinearTables(int4* ent, MatPtr* mat, const LinearPlan& p, int M, const cx_exl3_matrix* m, hipStream_t s) {
+  const MatPtr mp{m->tiles, reinterpret_cast<const __half*>(m->suh), reinterpret_cast<const __half*>(m->svh)};
+  // Entries beyond one block of threads loop: n_entries is at most M / 64 + 1.
+  for (int base = 0; base < p.n_entries; base += 1024) {
+    const int n = std::min(1024, p.n_entries - base);
+    hipLaunchKernelGGL(FillLinearTablesKernel, dim3(1), dim3(1024), 0, s, ent + base, mat, base, n, p.chunk, M, mp);
+  }
+}
+
+bool LaunchGemm(int k2, int cb, int nrb, int ksw, int u, dim3 grid, const GemmArgs& g, hipStream_t s) {
+  (void)u;
+  switch (k2) {
+    case 2: return LaunchGemmRate2(cb, nrb, ksw, grid, g, s);
+    case 3: return LaunchGemmRate3(cb, nrb, ksw, grid, g, s);
+    case 4: return LaunchGemmRate4(cb, nrb, ksw, grid, g, s);
+    case 5: return LaunchGemmRate5(cb, nrb, ksw, grid, g, s);
+    case 6: return LaunchGemmRate6(cb, nrb, ksw, grid, g, s);
+    case 7: return LaunchGemmRate7(cb, nrb, ksw, grid, g, s);
+    case 8: return LaunchGemmRate8(cb, nrb, ksw, grid, g, s);
+    case 10: return LaunchGemmRate10(cb, nrb, ksw, grid, g, s);
+    case 12: return LaunchGemmRate12(cb, nrb, ksw, grid, g, s);
+    case 14: return LaunchGemmRate14(cb, nrb, ksw, grid, g, s);
+    case 16: return LaunchGemmRate16(cb, nrb, ksw, grid, g, s);
+    default: return false;
+  }
+}
+
+size_t LinearWorkspace(const LinearPlan& p, int I, int O, int M) {
+  const size_t xp = AlignUp((size_t)M * I * 2, 256);
+  const size_t part = AlignUp((size_t)p.S * M * O * 4, 256);
+  const size_t ent = AlignUp((size_t)p.n_entries * 16, 256);
+  const size_t mat = AlignUp(sizeof(MatPtr), 256);
+  return xp + part + ent + mat;
+}
+
+}  // namespace cx
+
+using namespace cx;
+
+extern "C" {
+
+size_t cx_exl3_tile_bytes(int32_t in_features, int32_t out_features, int32_t k2) {
+  return (size_t)in_features * out_features * k2 / 16;
+}
+
+int cx_exl3_repack(const int16_t* trellis, int32_t in_features, int32_t out_features, int32_t k2, uint32_t* tiles,
+                   cx_stream_t stream) {
+  if (!trellis || !tiles) return CX_E_ARG;
+  if (in_features <= 0 || out_features <= 0 || in_features % 128 || out_features % 128) return CX_E_SHAPE;
+  if (!ValidK2(k2)) return CX_E_BITRATE;
+  const int A = in_features / 16, B = out_features / 16, T = TileDwords(k2);
+  const size_t total = (size_t)A * B * T;
+  const int grid = (int)std::min<size_t>((total + 255) / 256, 65536);
+  hipLaunchKernelGGL(RepackKernel, dim3(grid), dim3(256), 0, (hipStream_t)stream,
+                     reinterpret_cast<const uint32_t*>(trellis), tiles, A, B, T);
+  return LaunchStatus();
+}
+
+int cx_exl3_dequant(const cx_exl3_matrix* m, uint16_t* w_hat, cx_stream_t stream) {
+  int rc = CheckMatrix(m);
+  if (rc) return rc;
+  if (!w_hat) return CX_E_ARG;
+  const int A = m->in_features / 16, ncp = m->out_features / 32;
+  const dim3 grid((A * ncp + 3) / 4);
+  auto* w = reinterpret_cast<__half*>(w_hat);
+  bool ok = DispatchK2Cb(m->k2, m->codebook, [&](auto k2c, auto cbc) {
+    constexpr int K2 = decltype(k2c)::value, CB = decltype(cbc)::value;
+    hipLaunchKernelGGL((DequantKernel<K2, CB>), grid, dim3(256), 0, (hipStream_t)stream, m->tiles, w, A, ncp);
+  });
+  if (!ok) return CX_E_BITRATE;
+  return LaunchStatus();
+}
+
+size_t cx_exl3_linear_workspace_size(const cx_exl3_matrix* m, int32_t M) {
+  if (CheckMatrix(m) || M <= 0) return 0;
+  const LinearPlan p = PlanLinear(m->in_features, m->out_features, M);
+  return LinearWorkspace(p, m->in_features, m->out_features, M);
+}
+
+int cx_exl3_linear(const cx_exl3_matrix* m, const uint16_t* x, int32_t M, const int32_t* row_offsets,
+                   int32_t n_sessions, void* y, int32_t y_dtype, void* workspace, size_t workspace_bytes,
+                   cx_stream_t stream) {
+  int rc = CheckMatrix(m);
+  if (rc) return rc;
+  if (!x || !y || !workspace) return CX_E_ARG;
+  if (M <= 0) return CX_E_SHAPE;
+  if (y_dtype != CX_F16 && y_dtype != CX_F32) return CX_E_ARG;
+  if ((rc = RowOffsetsCheck(row_offsets, n_sessions, M))) return rc;
+  const int I = m->in_features, O = m->out_features;
+  const LinearPlan p = PlanLinear(I, O, M);
+  if (workspace_bytes < LinearWorkspace(p, I, O, M)) return CX_E_WORKSPACE;
+  hipStream_t s = (hipStream_t)stream;
+  char* ws = static_cast<char*>(workspace);
+  __half* xp = reinterpret_cast<__half*>(ws);
+  ws += AlignUp((size_t)M * I * 2, 256);
+  float* part = reinterpret_cast<float*>(ws);
+  ws += AlignUp((size_t)p.S * M * O * 4, 256);
+  int4* ent = reinterpret_cast<int4*>(ws);
+  ws += AlignUp((size_t)p.n_entries * 16, 256);
+  MatPtr* mat = reinterpret_cast<MatPtr*>(ws);
+
+  // Row entries and the matrix pointer go down with one tiny fill kernel each call, so
+  // the sequence holds no host-side state and no memset (graph-capturable).
+  FillLinearTables(ent, mat, p, M, m, s);
+  {
+    const int items = M * (I / 128);
+    hipLaunchKernelGGL(InputTransformKernel, dim3((items * 32 + 255) / 256), dim3(256), 0, s,
+                       reinterpret_cast<const __half*>(x), I, (const int*)nullptr,
+                       reinterpret_cast<const __half*>(m->suh), xp, M, I);
+  }
+  GemmArgs g{};
+  g.plane[0] = GemmPlane{mat, xp, part, I, O, (long long)M * O};
+  g.plane[1] = g.plane[0];
+  g.entries = ent;
+  g.n_entries = nullptr;
+  g.n_entries_host = p.n_entries;
+  g.A = p.A;
+  g.ncp = p.ncp;
+  g.S = p.S;
+  const dim3 grid(p.ncp / (4 / p.ksw) * p.S, p.n_entries, 1);
+  if (!LaunchGemm(m->k2, m->codebook, p.nrb, p.ksw, p.u, grid, g, s)) return CX_E_UNSUPPORTED;
+  {
+    const int items = M * (O / 128);
+    hipLaunchKernelGGL(OutputTransformKernel, dim3((items * 32 + 255) / 256), dim3(256), 0, s, part,
+                       (long long)M * O, p.S, reinterpret_cast<const __half*>(m->svh), y, M, O,
+                       y_dtype == CX_F16 ? 1 : 0);
+  }
+  return LaunchStatus();
+}
+
+const char* cx_version(void) { return "crucible-exl3-mi355x 0.1 (gfx950)"; }
+
+}  // extern "C"

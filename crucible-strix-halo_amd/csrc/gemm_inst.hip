@@ -1,0 +1,45 @@
+// Exl3GemmKernel instantiations for one rate (compiled once per rate with -DCX_RATE=K2).
+#include "internal.hpp"
+
+#ifndef CX_RATE
+#error "compile with -DCX_RATE=<2 x bits per weight>"
+#endif
+
+namespace cx {
+
+#define CX_CAT2(a, b) a##b
+#define CX_CAT(a, b) CX_CAT2(a, b)
+
+bool CX_CAT(LaunchGemmRate, CX_RATE)(int cb, int nrb, int ksw, dim3 grid, const GemmArgs& g, hipStream_t s) {
+  constexpr int K2 = CX_RATE;
+  constexpr int U = 4;
+  auto go = [&](auto cbc, auto nrbc, auto kswc) {
+    constexpr int CB = decltype(cbc)::value, NRB = decltype(nrbc)::value, KSW = decltype(kswc)::value;
+    hipLaunchKernelGGL((Exl3GemmKernel<K2, CB, NRB, KSW, U>), grid, dim3(256), 0, s, g);
+    return true;
+  };
+  auto rows = [&](auto cbc, auto kswc) {
+    switch (nrb) {
+      case 1: return go(cbc, IC<1>{}, kswc);
+      case 2: return go(cbc, IC<2>{}, kswc);
+      case 3: return go(cbc, IC<3>{}, kswc);
+      case 4: return go(cbc, IC<4>{}, kswc);
+      default: return false;
+    }
+  };
+  auto split = [&](auto cbc) {
+    if (ksw == 1) return rows(cbc, IC<1>{});
+    if (ksw == 4) return rows(cbc, IC<4>{});
+    return false;
+  };
+  if (cb == kCbMul1) return split(IC<kCbMul1>{});
+  if constexpr (K2 % 2 == 0) {
+    // Legacy codebooks: one 16-row block per wave, K split inside the workgroup.
+    if (nrb != 1 || ksw != 4) return false;
+    if (cb == kCbMcg) return go(IC<kCbMcg>{}, IC<1>{}, IC<4>{});
+    if (cb == kCb3Inst) return go(IC<kCb3Inst>{}, IC<1>{}, IC<4>{});
+  }
+  return false;
+}
+
+}  // namespace cx

@@ -1,0 +1,104 @@
+"""Python binding of libcrucible_exl3.so (the C-ABI in include/crucible_exl3.h).
+
+PyTorch is used only as device-memory and stream plumbing: every computation runs in
+the HIP library.  Loading fails loudly if the library is missing; there is no CPU or
+PyTorch fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+PKG_DIR = Path(__file__).resolve().parent.parent
+LIB_PATH = Path(os.environ.get("CX_LIB", PKG_DIR / "libcrucible_exl3.so"))
+
+CX_CB = {"3inst": 0, "mcg": 1, "mul1": 2}
+CX_F16, CX_F32 = 0, 1
+CX_MOE_AUTO, CX_MOE_DECODE, CX_MOE_PREFILL = 0, 1, 2
+ERRORS = {-1: "invalid argument", -2: "invalid shape", -3: "unsupported bitrate", -4: "workspace too small",
+          -5: "expert id out of range", -6: "unsupported combination"}
+
+EXPORTED = [
+    "cx_exl3_tile_bytes", "cx_exl3_repack", "cx_exl3_dequant", "cx_exl3_linear_workspace_size", "cx_exl3_linear",
+    "cx_moe_route", "cx_moe_group_workspace_size", "cx_moe_group", "cx_moe_plan_create", "cx_moe_plan_destroy",
+    "cx_moe_layer_workspace_size", "cx_moe_layer_forward", "cx_version",
+]
+
+
+class CxError(RuntimeError):
+    def __init__(self, fn: str, rc: int):
+        super().__init__(f"{fn} failed: {ERRORS.get(rc, f'HIP error {rc}')} ({rc})")
+        self.rc = rc
+
+
+class Matrix(ctypes.Structure):
+    _fields_ = [("tiles", ctypes.c_void_p), ("suh", ctypes.c_void_p), ("svh", ctypes.c_void_p),
+                ("in_features", ctypes.c_int32), ("out_features", ctypes.c_int32), ("k2", ctypes.c_int32),
+                ("codebook", ctypes.c_int32)]
+
+
+class Expert(ctypes.Structure):
+    _fields_ = [("gate", Matrix), ("up", Matrix), ("down", Matrix)]
+
+
+class Layer(ctypes.Structure):
+    _fields_ = [("hidden", ctypes.c_int32), ("intermediate", ctypes.c_int32), ("n_experts", ctypes.c_int32),
+                ("topk", ctypes.c_int32), ("experts", ctypes.POINTER(Expert)), ("shared", Expert)]
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"{LIB_PATH} is not built: run __graft_entry__.build() (make -C crucible-strix-halo_amd)")
+        L = ctypes.CDLL(str(LIB_PATH))
+        P, I32, SZ = ctypes.c_void_p, ctypes.c_int32, ctypes.c_size_t
+        L.cx_exl3_tile_bytes.argtypes = [I32, I32, I32]
+        L.cx_exl3_tile_bytes.restype = SZ
+        L.cx_exl3_repack.argtypes = [P, I32, I32, I32, P, P]
+        L.cx_exl3_dequant.argtypes = [ctypes.POINTER(Matrix), P, P]
+        L.cx_exl3_linear_workspace_size.argtypes = [ctypes.POINTER(Matrix), I32]
+        L.cx_exl3_linear_workspace_size.restype = SZ
+        L.cx_exl3_linear.argtypes = [ctypes.POINTER(Matrix), P, I32, P, I32, P, I32, P, SZ, P]
+        L.cx_moe_route.argtypes = [P, I32, I32, I32, I32, P, P, P, P]
+        L.cx_moe_group_workspace_size.argtypes = [I32, I32, I32]
+        L.cx_moe_group_workspace_size.restype = SZ
+        L.cx_moe_group.argtypes = [P, I32, I32, I32, P, P, P, P, P, SZ, P]
+        L.cx_moe_plan_create.argtypes = [ctypes.POINTER(Layer), ctypes.POINTER(ctypes.c_void_p)]
+        L.cx_moe_plan_destroy.argtypes = [P]
+        L.cx_moe_plan_destroy.restype = None
+        L.cx_moe_layer_workspace_size.argtypes = [P, I32, I32]
+        L.cx_moe_layer_workspace_size.restype = SZ
+        L.cx_moe_layer_forward.argtypes = [P, P, P, I32, P, I32, P, I32, P, P, P, I32, P, SZ, P]
+        L.cx_version.restype = ctypes.c_char_p
+        for fn in ("cx_exl3_repack", "cx_exl3_dequant", "cx_exl3_linear", "cx_moe_route", "cx_moe_group",
+                   "cx_moe_plan_create", "cx_moe_layer_forward"):
+            getattr(L, fn).restype = ctypes.c_int
+        _lib = L
+    return _lib
+
+
+def check(fn: str, rc: int) -> None:
+    if rc != 0:
+        raise CxError(fn, rc)
+
+
+def ptr(t) -> int | None:
+    """Device pointer of a torch tensor (None passes through)."""
+    return None if t is None else t.data_ptr()
+
+
+def stream_ptr(stream=None):
+    import torch
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return ctypes.c_void_p(s.cuda_stream)
+
+
+def i32_host(values) -> ctypes.Array | None:
+    if values is None:
+        return None
+    return (ctypes.c_int32 * len(values))(*[int(v) for v in values])

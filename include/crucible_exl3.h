@@ -1,0 +1,147 @@
+/*
+ * crucible_exl3.h — C-ABI of the MI355X (gfx950) EXL3 quantized MoE expert path.
+ *
+ * Drop-in boundary for Crucible's EXL3 linear op and MoE layer (the reference is the
+ * engine's in-process C++: file:line citations are relative to the reference root).
+ * All pointers are device pointers unless a parameter says "host".  Every call is
+ * asynchronous on the given HIP stream, allocates nothing (workspace is caller
+ * memory, sized by the matching *_workspace_size query), never exits, and returns:
+ *     0  success
+ *    <0  invalid argument or shape (CX_E_*)
+ *    >0  a hipError_t from a launch
+ *
+ * fp16 data is passed as uint16_t bit patterns (IEEE binary16).
+ */
+#ifndef CRUCIBLE_EXL3_H
+#define CRUCIBLE_EXL3_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* cx_stream_t; /* a hipStream_t; NULL = the null stream */
+
+enum {
+  CX_OK = 0,
+  CX_E_ARG = -1,       /* null pointer or bad enum */
+  CX_E_SHAPE = -2,     /* dimension not a multiple of 128, rows out of range, ... */
+  CX_E_BITRATE = -3,   /* bits per weight not in 1..8 or 1.5 / 2.5 / 3.5 */
+  CX_E_WORKSPACE = -4, /* workspace too small */
+  CX_E_EXPERT = -5,    /* expert id out of range */
+  CX_E_UNSUPPORTED = -6
+};
+
+enum { CX_CB_3INST = 0, CX_CB_MCG = 1, CX_CB_MUL1 = 2 };   /* codebook, docs/EXL3_FORMAT.md §3 */
+enum { CX_F16 = 0, CX_F32 = 1 };                            /* activation dtypes */
+enum { CX_MOE_AUTO = 0, CX_MOE_DECODE = 1, CX_MOE_PREFILL = 2 };
+
+/* One EXL3 linear [in_features x out_features] on the device, with its tiles already in
+ * this library's layout (cx_exl3_repack).  Replaces the weight half of
+ * `LinJob{tiles,suh,svh,...,I,O,K}` (engine/exl3/exl3.h:20-33) and `Lin`
+ * (engine/model/flashnext/model.h:40-46). */
+typedef struct cx_exl3_matrix {
+  const uint32_t* tiles;   /* column-pair-major tiles, 8K dwords each */
+  const uint16_t* suh;     /* fp16 [in_features] input sign/scale */
+  const uint16_t* svh;     /* fp16 [out_features] output sign/scale */
+  int32_t in_features;     /* multiple of 128 */
+  int32_t out_features;    /* multiple of 128 */
+  int32_t k2;              /* 2 x bits per weight: 2..16, or 3 / 5 / 7 for K = 1.5 / 2.5 / 3.5 */
+  int32_t codebook;        /* CX_CB_* */
+} cx_exl3_matrix;
+
+/* Bytes of a matrix's packed tiles (I * O * K / 8). */
+size_t cx_exl3_tile_bytes(int32_t in_features, int32_t out_features, int32_t k2);
+
+/* Loader repack: checkpoint trellis [I/16][O/16][16K] int16 (docs/EXL3_FORMAT.md §1-2)
+ * -> this library's column-pair-major tiles.  Replaces the loader's trellis repack to
+ * "crucible order" (engine/model/flashnext/model.h:503-527).  src and dst must not overlap. */
+int cx_exl3_repack(const int16_t* trellis, int32_t in_features, int32_t out_features, int32_t k2,
+                   uint32_t* tiles, cx_stream_t stream);
+
+/* Dequantize to the rotated-basis fp16 W_hat [I][O] (bit-exact decoded weights).  The
+ * parity hook for ref/exl3_ref.py:110-119 `reconstruct_inner`. */
+int cx_exl3_dequant(const cx_exl3_matrix* m, uint16_t* w_hat, cx_stream_t stream);
+
+/* y = EXL3 linear of M packed activation rows.  Replaces `Build` + `RunGroup`
+ * (engine/engine.hip:1046, 1731) over one `LinJob` with R = M rows, i.e. LinInKernel
+ * -> split-K GEMV -> LinOutKernel (engine/exl3/exl3.h:48-82, 330-389).
+ *   x         fp16 [M][in_features]
+ *   row_offsets  host, nullable: n_sessions + 1 exclusive prefix sums of the rows each
+ *             session packed (ragged verify spans); checked, must end at M
+ *   y_dtype   CX_F32: y_h kept fp32 through the output transform (engine LinOutBlock);
+ *             CX_F16: y_h rounded to fp16 before it (ref/exl3_ref.py:175 default)
+ *   workspace device scratch of cx_exl3_linear_workspace_size(m, M) bytes */
+size_t cx_exl3_linear_workspace_size(const cx_exl3_matrix* m, int32_t M);
+int cx_exl3_linear(const cx_exl3_matrix* m, const uint16_t* x, int32_t M, const int32_t* row_offsets,
+                   int32_t n_sessions, void* y, int32_t y_dtype, void* workspace, size_t workspace_bytes,
+                   cx_stream_t stream);
+
+/* Router: top-k of E fp32 logits per row (logit descending, lower id on ties), the
+ * selection softmax w_k = exp(l_k - l_0) / sum_j exp(l_j - l_0), and w_topk =
+ * sigmoid(shared logit).  Replaces MoeRouteKernel (engine/layers/ops.h:683-713) and
+ * PrefillMoeRouteWaveKernel (engine/layers/prefill_moe.h:567-615).
+ *   logits        fp32 [M][ld], ld >= E
+ *   shared_logit  fp32 [M], nullable: then column E of logits (ld >= E + 1), the
+ *                 engine's [M][E+1] router output layout
+ *   sel int32 [M][topk], wts fp32 [M][topk + 1] */
+int cx_moe_route(const float* logits, int32_t ld, int32_t M, int32_t E, int32_t topk, const float* shared_logit,
+                 int32_t* sel, float* wts, cx_stream_t stream);
+
+/* Stable expert-major grouping with on-device prefix sums (no host round trip).
+ * counts [E], exclusive offsets [E+1], pairs [M*topk] (row * topk + slot, stable by
+ * route index), row_ids [M*topk] (pairs / topk).  Replaces the MoeDispatch kernels
+ * (engine/layers/kernels/prefill_moe.h:9-100); oracle ref/prefill_ref.py:37-45. */
+size_t cx_moe_group_workspace_size(int32_t M, int32_t E, int32_t topk);
+int cx_moe_group(const int32_t* sel, int32_t M, int32_t E, int32_t topk, int32_t* counts, int32_t* offsets,
+                 int32_t* pairs, int32_t* row_ids, void* workspace, size_t workspace_bytes, cx_stream_t stream);
+
+/* A SwiGLU expert: gate [H][I], up [H][I], down [I][H].  Replaces `ExpertPtrs`
+ * (engine/layers/ops.h:673-678). */
+typedef struct cx_moe_expert {
+  cx_exl3_matrix gate, up, down;
+} cx_moe_expert;
+
+/* One MoE layer.  `experts` is a HOST array of E routed experts; the shared expert is
+ * always on (slot topk).  Every routed expert must share the gate/up and the down
+ * bitrate and codebook (the shared expert may differ).  Replaces `Moe`
+ * (engine/model/flashnext/model.h:71-76). */
+typedef struct cx_moe_layer {
+  int32_t hidden;        /* H, multiple of 128 */
+  int32_t intermediate;  /* I, multiple of 128 */
+  int32_t n_experts;     /* E */
+  int32_t topk;          /* k */
+  const cx_moe_expert* experts; /* host [E] */
+  cx_moe_expert shared;
+} cx_moe_layer;
+
+/* Prepared (device-resident) expert tables of a layer: built once, reused by every
+ * call.  Replaces the d_experts upload (engine/model/flashnext/model.h:75). */
+typedef struct cx_moe_plan cx_moe_plan;
+int cx_moe_plan_create(const cx_moe_layer* layer, cx_moe_plan** plan);
+void cx_moe_plan_destroy(cx_moe_plan* plan);
+
+/* y = MoE layer over M packed rows: route, group, gate/up, SiLU * up, down, and the
+ * weighted combine (routed slots in selection order, shared expert last, fp32).
+ * Replaces Engine::BlockMoe (engine/engine.hip:1327-1342, decode) and the MoE half of
+ * Engine::PrefillBlock (engine/runtime/prefill_engine.inc:365-435, prefill).
+ *   x             fp16 [M][H] hidden states
+ *   logits        fp32 [M][ld] router logits (see cx_moe_route for shared_logit)
+ *   row_offsets   host, nullable: session prefix sums, checked, must end at M
+ *   y             fp32 [M][H]
+ *   sel, wts      nullable outputs: int32 [M][topk] and fp32 [M][topk + 1]
+ *   mode          CX_MOE_DECODE / PREFILL / AUTO (by M) */
+size_t cx_moe_layer_workspace_size(const cx_moe_plan* plan, int32_t M, int32_t mode);
+int cx_moe_layer_forward(const cx_moe_plan* plan, const uint16_t* x, const float* logits, int32_t ld,
+                 const float* shared_logit, int32_t M, const int32_t* row_offsets, int32_t n_sessions, float* y,
+                 int32_t* sel, float* wts, int32_t mode, void* workspace, size_t workspace_bytes, cx_stream_t stream);
+
+/* Library version string. */
+const char* cx_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* CRUCIBLE_EXL3_H */

@@ -1,0 +1,135 @@
+"""GPU parity of the EXL3 decode and linear op (C-ABI, HIP kernels) against the CPU oracle.
+Dequantized weights: bit-exact.  Linear outputs: rel-L2 <= 1e-3 (fp32 and fp16 outputs)
+and max |err| <= 1e-3 * max |y| reported; rows bitwise invariant to M."""
+import numpy as np
+import pytest
+
+import oracle as O
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+RATES = [1, 1.5, 2, 2.5, 3, 3.5, 4, 5, 6, 7, 8]
+
+
+@pytest.fixture(scope="module")
+def ops():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from exl3moe import ops as _ops
+    return _ops
+
+
+def rel_l2(a, b):
+    a = np.asarray(a, dtype=np.float64)
+    b = np.asarray(b, dtype=np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+@pytest.mark.parametrize("bits", RATES)
+def test_dequant_bit_exact_all_rates(ops, bits):
+    from exl3moe import synth
+    rng = np.random.default_rng(100 + int(bits * 2))
+    tr, suh, svh = synth.linear(rng, 256, 384, bits)
+    lin = ops.DeviceLinear.from_trellis(tr, suh, svh, bits)
+    got = lin.dequant().cpu().numpy()
+    want = O.reconstruct_inner(tr, bits, "mul1")
+    np.testing.assert_array_equal(got.view(np.uint16), want.view(np.uint16))
+
+
+@pytest.mark.parametrize("bits,cb", [(4, "mcg"), (3, "3inst"), (2, "mcg"), (8, "3inst")])
+def test_dequant_bit_exact_other_codebooks(ops, bits, cb):
+    from exl3moe import synth
+    rng = np.random.default_rng(7)
+    tr, suh, svh = synth.linear(rng, 128, 256, bits)
+    lin = ops.DeviceLinear.from_trellis(tr, suh, svh, bits, codebook=cb)
+    got = lin.dequant().cpu().numpy()
+    np.testing.assert_array_equal(got.view(np.uint16), O.reconstruct_inner(tr, bits, cb).view(np.uint16))
+
+
+def test_config1_linear_2048x512(ops):
+    # 2048 -> 512 at 4 bpw, x fp16 [1][2048] ~ N(0, 1).
+    from exl3moe import synth
+    rng = np.random.default_rng(1)
+    tr, suh, svh = synth.linear(rng, 2048, 512, 4)
+    lin = ops.DeviceLinear.from_trellis(tr, suh, svh, 4)
+    w = O.reconstruct_inner(tr, 4)
+    np.testing.assert_array_equal(lin.dequant().cpu().numpy().view(np.uint16), w.view(np.uint16))
+    x = rng.standard_normal((1, 2048)).astype(np.float16)
+    xt = torch.from_numpy(x).cuda()
+    y32 = lin(xt, torch.float32).cpu().numpy()
+    y16 = lin(xt, torch.float16).cpu().numpy()
+    r32 = O.matvec(x, w, suh, svh, np.float32)
+    r16 = O.matvec(x, w, suh, svh, np.float16)
+    e32, e16 = rel_l2(y32, r32), rel_l2(y16, r16)
+    print(f"config1 rel_l2 f32={e32:.3e} f16={e16:.3e} max_abs f32={np.abs(y32 - r32).max():.3e}")
+    assert e32 <= 1e-3 and e16 <= 1e-3
+    assert np.abs(y32 - r32).max() <= 1e-3 * np.abs(r32).max()
+
+
+@pytest.mark.parametrize("I,O_", [(2048, 4096), (4096, 2048)])
+def test_config2_ragged_gemv(ops, I, O_):
+    # 8 sessions x (1 + d) rows, d ~ U{0..4} -> 8..40 rows, 4 bpw.
+    from exl3moe import synth
+    rng = np.random.default_rng(2 + I)
+    tr, suh, svh = synth.linear(rng, I, O_, 4)
+    lin = ops.DeviceLinear.from_trellis(tr, suh, svh, 4)
+    w = O.reconstruct_inner(tr, 4)
+    offs = synth.sessions(rng, 8, 1, 5)
+    M = offs[-1]
+    x = rng.standard_normal((M, I)).astype(np.float16)
+    y = lin(torch.from_numpy(x).cuda(), torch.float32, row_offsets=offs).cpu().numpy()
+    ref = O.matvec(x, w, suh, svh, np.float32)
+    e = rel_l2(y, ref)
+    print(f"config2 {I}->{O_} M={M} rel_l2={e:.3e} max_abs={np.abs(y - ref).max():.3e}")
+    assert e <= 1e-3
+    assert np.abs(y - ref).max() <= 1e-3 * np.abs(ref).max()
+
+
+@pytest.mark.parametrize("bits", [1.5, 2.5, 3, 5, 6, 7, 8])
+def test_linear_other_rates(ops, bits):
+    from exl3moe import synth
+    rng = np.random.default_rng(int(bits * 10))
+    tr, suh, svh = synth.linear(rng, 512, 256, bits)
+    lin = ops.DeviceLinear.from_trellis(tr, suh, svh, bits)
+    x = rng.standard_normal((19, 512)).astype(np.float16)
+    y = lin(torch.from_numpy(x).cuda(), torch.float32).cpu().numpy()
+    ref = O.matvec(x, O.reconstruct_inner(tr, bits), suh, svh, np.float32)
+    assert rel_l2(y, ref) <= 1e-3
+
+
+def test_rows_invariant_to_batch(ops):
+    # A row's output is bitwise the same whatever other rows share the call.
+    from exl3moe import synth
+    rng = np.random.default_rng(5)
+    tr, suh, svh = synth.linear(rng, 2048, 1024, 4)
+    lin = ops.DeviceLinear.from_trellis(tr, suh, svh, 4)
+    x = torch.from_numpy(rng.standard_normal((70, 2048)).astype(np.float16)).cuda()
+    full = lin(x).cpu().numpy()
+    for M in (1, 3, 17, 40):
+        part = lin(x[:M].contiguous()).cpu().numpy()
+        np.testing.assert_array_equal(part.view(np.uint32), full[:M].view(np.uint32))
+
+
+def test_linear_large_m_prefill_rows(ops):
+    from exl3moe import synth
+    rng = np.random.default_rng(8)
+    tr, suh, svh = synth.linear(rng, 1024, 512, 3)
+    lin = ops.DeviceLinear.from_trellis(tr, suh, svh, 3)
+    x = rng.standard_normal((300, 1024)).astype(np.float16)
+    y = lin(torch.from_numpy(x).cuda()).cpu().numpy()
+    ref = O.matvec(x, O.reconstruct_inner(tr, 3), suh, svh, np.float32)
+    assert rel_l2(y, ref) <= 1e-3
+
+
+def test_linear_errors(ops):
+    from exl3moe import CxError, synth
+    rng = np.random.default_rng(9)
+    tr, suh, svh = synth.linear(rng, 256, 128, 4)
+    lin = ops.DeviceLinear.from_trellis(tr, suh, svh, 4)
+    x = torch.zeros(3, 256, dtype=torch.float16, device="cuda")
+    with pytest.raises(CxError):
+        lin(x, row_offsets=[0, 1, 2])  # offsets end at 2, not 3
+    small = torch.empty(16, dtype=torch.uint8, device="cuda")
+    with pytest.raises(CxError):
+        lin(x, workspace=small)
