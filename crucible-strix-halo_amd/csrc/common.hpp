@@ -10,6 +10,7 @@ namespace cx {
 
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef unsigned short ushort2_t __attribute__((ext_vector_type(2)));
 
@@ -48,6 +49,12 @@ __device__ __forceinline__ void Wht128x4(float v[4]) {
 // [.., 4q + s, ..] with row(q, s) = 2q + (s & 1) + 8 (s >> 1).
 __host__ __device__ constexpr int PermPos16(int r) { return 4 * ((r & 7) >> 1) + (r & 1) + 2 * (r >> 3); }
 __host__ __device__ constexpr int PermRow16(int p) { return 2 * (p >> 2) + (p & 1) + 8 * ((p >> 1) & 1); }
+// The same for a 16x16x32 MFMA over two k-tiles (32 input rows): lane group q holds
+// slots 8q..8q+7 = rows {2q, 2q+1, 2q+8, 2q+9} of the first k-tile, then of the second.
+__host__ __device__ constexpr int PermPos32(int r) { return 8 * ((r & 7) >> 1) + 4 * (r >> 4) + (r & 1) + 2 * ((r >> 3) & 1); }
+__host__ __device__ constexpr int PermRow32(int p) {
+  return 16 * ((p >> 2) & 1) + 2 * (p >> 3) + (p & 1) + 8 * ((p >> 1) & 1);
+}
 
 // Raw buffer resource over [base, base + bytes): loads past the end return zero.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t MakeRsrc(const void* base, uint32_t bytes) {
@@ -57,8 +64,41 @@ __device__ __forceinline__ uint32_t BufLoad32(__amdgpu_buffer_rsrc_t r, uint32_t
   return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
 }
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x3_t __attribute__((ext_vector_type(3)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ u32x2_t BufLoad64(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
   return __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
+}
+__device__ __forceinline__ u32x4_t BufLoad128(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+}
+// N consecutive dwords (N = 1..4) from a buffer.
+template <int N>
+struct Dwords {
+  uint32_t v[N];
+};
+template <int N>
+__device__ __forceinline__ Dwords<N> BufLoadN(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  Dwords<N> d;
+  if constexpr (N == 1) {
+    d.v[0] = __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+  } else if constexpr (N == 2) {
+    const u32x2_t t = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
+    d.v[0] = t.x;
+    d.v[1] = t.y;
+  } else if constexpr (N == 3) {
+    const u32x3_t t = __builtin_amdgcn_raw_buffer_load_b96(r, voff, soff, 0);
+    d.v[0] = t.x;
+    d.v[1] = t.y;
+    d.v[2] = t.z;
+  } else {
+    const u32x4_t t = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+    d.v[0] = t.x;
+    d.v[1] = t.y;
+    d.v[2] = t.z;
+    d.v[3] = t.w;
+  }
+  return d;
 }
 
 }  // namespace cx

@@ -76,7 +76,7 @@ __global__ void __launch_bounds__(256) InputTransformKernel(const __half* __rest
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int e = 4 * j + i;
-    d[(e & ~15) + PermPos16(e & 15)] = __float2half(v[i] * kHadNorm);
+    d[(e & ~31) + PermPos32(e & 31)] = __float2half(v[i] * kHadNorm);
   }
 }
 
@@ -148,8 +148,9 @@ LinearPlan PlanLinear(int I, int O, int M) {
   // whatever other rows share the call.
   p.S = 1;
   const int wgs = p.ncp;
-  while (wgs * p.S < 512 && p.A % (p.ksw * p.S * 2) == 0 && p.A / (p.ksw * p.S * 2) >= 4) p.S *= 2;
-  const int steps = p.A / (p.ksw * p.S);
+  // Steps are two k-tiles; keep at least 4 steps per wave.
+  while (wgs * p.S < 512 && (p.A / 2) / (p.ksw * p.S * 2) >= 4) p.S *= 2;
+  const int steps = p.A / 2 / (p.ksw * p.S);
   p.u = steps % 4 == 0 ? 4 : steps % 2 == 0 ? 2 : 1;
   return p;
 }

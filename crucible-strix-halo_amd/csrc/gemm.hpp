@@ -6,6 +6,13 @@
 //   tile (a, b) -> tile index ((b / 2) * A + a) * 2 + (b % 2),  8K dwords per tile.
 // A wave walks one column pair down K, so every wave's weight stream is contiguous.
 //
+// A step is two k-tiles of one column pair: 4 tiles, contiguous in HBM.  Each lane
+// loads a contiguous slice of the step (coalesced, no lane reads a byte twice) into the
+// wave's LDS slot; each lane then reads the window dwords of its two runs (run t of the
+// step's first and second k-tile) back from LDS, decodes 16 weights and feeds two
+// v_mfma_f32_16x16x32_f16 (columns c and c + 8 of its tile).  Activations are stored
+// in the matching 32-row order (PermPos32), one 16-byte load per lane and 16-row block.
+//
 // Work item (one 256-thread workgroup = 4 waves):
 //   blockIdx.x -> (column-pair group, K segment), blockIdx.y -> row entry
 //   {matrix, first row, rows}, blockIdx.z -> plane (e.g. gate / up).
@@ -37,6 +44,7 @@ struct GemmArgs {
   const int4* entries;   // {matrix, row0, nrows, unused}
   const int* n_entries;  // device-side count (nullptr: use n_entries_host)
   int n_entries_host;
+  int entry_base;        // blockIdx.y + entry_base indexes entries
   int A;    // k-tiles (I / 16)
   int ncp;  // column pairs (O / 32)
   int S;    // K segments across workgroups
@@ -45,93 +53,109 @@ struct GemmArgs {
 template <int K2, int CB, int NRB, int KSW, int U>
 __global__ void __launch_bounds__(256) Exl3GemmKernel(GemmArgs g) {
   constexpr int CPW = 4 / KSW;
-  constexpr int T = TileDwords(K2);
+  constexpr int T = TileDwords(K2);    // dwords per tile
+  constexpr int SD = 4 * T;            // dwords per step
+  constexpr int DPL = (SD + 63) / 64;  // dwords each lane loads per step
   constexpr int ND = WindowDwords(K2);
+  __shared__ uint32_t stage[4][64 * DPL];
   const int n_entries = g.n_entries ? *g.n_entries : g.n_entries_host;
-  if ((int)blockIdx.y >= n_entries) return;
-  const int4 ent = g.entries[blockIdx.y];
+  const int ei = (int)blockIdx.y + g.entry_base;
+  if (ei >= n_entries) return;
+  const int4 ent = g.entries[ei];
   const GemmPlane& pl = g.plane[blockIdx.z];
   const int ncpg = g.ncp / CPW;
   const int cpg = blockIdx.x % ncpg, kseg = blockIdx.x / ncpg;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int cp = cpg * CPW + wave / KSW, ks = wave % KSW;
   const int nsplit = g.S * KSW, split = kseg * KSW + ks;
-  const int a0 = g.A * split / nsplit, a1 = g.A * (split + 1) / nsplit;
-  const int steps = a1 - a0;
+  const int A2 = g.A / 2;
+  const int s0 = A2 * split / nsplit, s1 = A2 * (split + 1) / nsplit;
+  const int steps = s1 - s0, a0 = 2 * s0;
   const int row0 = ent.y, nrows = ent.z;
   const MatPtr m = pl.mats[ent.x];
 
-  const __amdgpu_buffer_rsrc_t rw = MakeRsrc(m.tiles + ((size_t)cp * g.A + a0) * 2 * T, (uint32_t)steps * 2 * T * 4);
+  const __amdgpu_buffer_rsrc_t rw = MakeRsrc(m.tiles + ((size_t)cp * g.A + a0) * 2 * T, (uint32_t)steps * SD * 4);
   const __amdgpu_buffer_rsrc_t rx = MakeRsrc(pl.x + (size_t)row0 * pl.ldx, (uint32_t)nrows * pl.ldx * 2);
   const LaneRun<K2> lr(lane);
-  uint32_t woff[ND];
+  // LDS dword offsets of the lane's windows: run t of tile (k-tile j, column tile tau).
+  uint32_t woff[2][ND];
 #pragma unroll
-  for (int i = 0; i < ND; ++i) woff[i] = lr.ByteOffset(i);
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int i = 0; i < ND; ++i) woff[j][i] = (uint32_t)((2 * j + lr.tile) * T + (lr.d0 + i) % T);
+  const uint32_t loff = (uint32_t)lane * DPL * 4;
   uint32_t xoff[NRB];
 #pragma unroll
-  for (int rb = 0; rb < NRB; ++rb) xoff[rb] = (uint32_t)(((rb * 16 + (lane & 15)) * pl.ldx + a0 * 16 + 4 * (lane >> 4)) * 2);
+  for (int rb = 0; rb < NRB; ++rb) xoff[rb] = (uint32_t)(((rb * 16 + (lane & 15)) * pl.ldx + a0 * 16 + 8 * (lane >> 4)) * 2);
+  uint32_t* slot = stage[wave];
 
   float4_t acc[NRB][2];
 #pragma unroll
   for (int rb = 0; rb < NRB; ++rb) acc[rb][0] = acc[rb][1] = float4_t{0.f, 0.f, 0.f, 0.f};
 
-  uint32_t wa[U][ND], wb[U][ND];
-  u32x2_t xa[U][NRB], xb[U][NRB];
-  auto load = [&](uint32_t (&w)[U][ND], u32x2_t (&x)[U][NRB], int s0) {
+  auto load_w = [&](int s) { return BufLoadN<DPL>(rw, loff, (uint32_t)s * SD * 4); };
+  auto load_x = [&](int s, int rb) { return BufLoad128(rx, xoff[rb], (uint32_t)s * 64); };
+  auto step = [&](const Dwords<DPL>& w, const u32x4_t (&x)[NRB]) {
+    // Stage the step in the wave's slot; LDS executes a wave's operations in order, so
+    // the window reads below see these writes and the next step's writes follow them.
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const uint32_t sw = (uint32_t)(s0 + u) * 2 * T * 4, sx = (uint32_t)(s0 + u) * 32;
+    for (int i = 0; i < DPL; ++i) slot[lane * DPL + i] = w.v[i];
+    __builtin_amdgcn_wave_barrier();
+    uint32_t v[2][3];
 #pragma unroll
-      for (int i = 0; i < ND; ++i) w[u][i] = BufLoad32(rw, woff[i], sw);
+    for (int j = 0; j < 2; ++j) {
 #pragma unroll
-      for (int rb = 0; rb < NRB; ++rb) x[u][rb] = BufLoad64(rx, xoff[rb], sx);
+      for (int i = 0; i < ND; ++i) v[j][i] = slot[woff[j][i]];
+      if constexpr (ND == 2) v[j][2] = 0u;
+    }
+    __builtin_amdgcn_wave_barrier();
+    half4_t lo0, hi0, lo1, hi1;
+    DecodeRun<K2, CB>(v[0][0], v[0][1], v[0][2], lr.shift, lo0, hi0);
+    DecodeRun<K2, CB>(v[1][0], v[1][1], v[1][2], lr.shift, lo1, hi1);
+    const half8_t b0 = {lo0[0], lo0[1], lo0[2], lo0[3], lo1[0], lo1[1], lo1[2], lo1[3]};
+    const half8_t b1 = {hi0[0], hi0[1], hi0[2], hi0[3], hi1[0], hi1[1], hi1[2], hi1[3]};
+#pragma unroll
+    for (int rb = 0; rb < NRB; ++rb) {
+      const half8_t av = __builtin_bit_cast(half8_t, x[rb]);
+      acc[rb][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b0, acc[rb][0], 0, 0, 0);
+      acc[rb][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b1, acc[rb][1], 0, 0, 0);
     }
   };
-  auto compute = [&](uint32_t (&w)[U][ND], u32x2_t (&x)[U][NRB]) {
+
+  // Register double buffering: the loads of the next U steps are in flight while the
+  // current U steps are decoded; then the remaining (< U) steps one at a time.
+  Dwords<DPL> wa[U], wb[U];
+  u32x4_t xa[U][NRB], xb[U][NRB];
+  auto load_group = [&](Dwords<DPL> (&w)[U], u32x4_t (&x)[U][NRB], int sb) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      half4_t blo, bhi;
-      DecodeRun<K2, CB>(w[u][0], w[u][1], ND > 2 ? w[u][ND - 1] : 0u, lr.shift, blo, bhi);
+      w[u] = load_w(sb + u);
 #pragma unroll
-      for (int rb = 0; rb < NRB; ++rb) {
-        const half4_t av = __builtin_bit_cast(half4_t, x[u][rb]);
-        acc[rb][0] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, blo, acc[rb][0], 0, 0, 0);
-        acc[rb][1] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, bhi, acc[rb][1], 0, 0, 0);
-      }
+      for (int rb = 0; rb < NRB; ++rb) x[u][rb] = load_x(sb + u, rb);
     }
   };
-  // Two register sets: decode one group of U steps while the next is in flight, then
-  // the remaining (< U) steps one at a time.
   int s = 0;
-  if (steps >= U) load(wa, xa, 0);
+  if (steps >= U) load_group(wa, xa, 0);
   while (s + U <= steps) {
     const bool more = s + 2 * U <= steps;
-    if (more) load(wb, xb, s + U);
-    compute(wa, xa);
+    if (more) load_group(wb, xb, s + U);
+#pragma unroll
+    for (int u = 0; u < U; ++u) step(wa[u], xa[u]);
     s += U;
     if (!more) break;
     const bool more2 = s + 2 * U <= steps;
-    if (more2) load(wa, xa, s + U);
-    compute(wb, xb);
+    if (more2) load_group(wa, xa, s + U);
+#pragma unroll
+    for (int u = 0; u < U; ++u) step(wb[u], xb[u]);
     s += U;
     if (!more2) break;
   }
   for (; s < steps; ++s) {
-    uint32_t w1[1][ND];
-    u32x2_t x1[1][NRB];
-    const uint32_t sw = (uint32_t)s * 2 * T * 4, sx = (uint32_t)s * 32;
+    const Dwords<DPL> w1 = load_w(s);
+    u32x4_t x1[NRB];
 #pragma unroll
-    for (int i = 0; i < ND; ++i) w1[0][i] = BufLoad32(rw, woff[i], sw);
-#pragma unroll
-    for (int rb = 0; rb < NRB; ++rb) x1[0][rb] = BufLoad64(rx, xoff[rb], sx);
-    half4_t blo, bhi;
-    DecodeRun<K2, CB>(w1[0][0], w1[0][1], ND > 2 ? w1[0][ND - 1] : 0u, lr.shift, blo, bhi);
-#pragma unroll
-    for (int rb = 0; rb < NRB; ++rb) {
-      const half4_t av = __builtin_bit_cast(half4_t, x1[0][rb]);
-      acc[rb][0] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, blo, acc[rb][0], 0, 0, 0);
-      acc[rb][1] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, bhi, acc[rb][1], 0, 0, 0);
-    }
+    for (int rb = 0; rb < NRB; ++rb) x1[rb] = load_x(s, rb);
+    step(w1, x1);
   }
 
   if constexpr (KSW > 1) {

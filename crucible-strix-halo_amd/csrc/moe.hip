@@ -1,20 +1,664 @@
-// MoE layer path (route, group, expert GEMMs, combine).
+// EXL3 MoE layer on MI355X: router top-k, stable expert-major grouping built on the
+// device (prefix sums and GEMM work lists, no host round trip), per-expert input
+// transforms, grouped gate/up decode-GEMM, mid (SiLU * up + down input transform),
+// grouped down decode-GEMM, and the weighted combine with the shared expert.
+//
+// Row space of one call with M rows and top-k routing: P = M k + M "compact rows".
+// Rows [0, M k) are the routed (row, slot) pairs in stable expert-major order (pairs[]),
+// rows [M k, M k + M) are the shared expert's rows 0..M-1.  Every expert's rows are
+// contiguous, so an expert GEMM reads one contiguous block of activation rows.
+#include <cstdlib>
+#include <new>
+
 #include "internal.hpp"
 
+namespace cx {
+
+constexpr int kMaxExperts = 1024;
+constexpr int kMaxTopK = 32;
+constexpr int kSmallRoutes = 2048;  // single-workgroup grouping up to this many routes
+
+// ---- router ---------------------------------------------------------------------------
+
+// One wave per row: top-k of E logits by repeated wave argmax (logit descending, lower
+// id on ties), then the selection softmax exp(l_k - l_0) / sum_j exp(l_j - l_0) summed in
+// rank order, and sigmoid of the shared logit.  engine/layers/ops.h:683-713.
+__global__ void __launch_bounds__(256) RouteKernel(const float* __restrict__ logits, int ld, int M, int E, int topk,
+                                                   const float* __restrict__ shared_logit, int* __restrict__ sel,
+                                                   float* __restrict__ wts) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= M) return;
+  const int lane = threadIdx.x & 63;
+  const float* lg = logits + (size_t)row * ld;
+  constexpr int V = kMaxExperts / 64;
+  float v[V];
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    const int e = i * 64 + lane;
+    v[i] = e < E ? lg[e] : -INFINITY;
+  }
+  unsigned taken = 0;  // bit i: this lane's value i is already selected
+  float sl0 = 0.f, sum = 0.f;
+  float mine = 0.f;  // lane k < topk keeps the logit of rank k
+  for (int k = 0; k < topk; ++k) {
+    // Lane-local best among values not taken: value desc, id asc.
+    float bv = -INFINITY;
+    int be = 0x7fffffff;
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const int e = i * 64 + lane;
+      if (e < E && !((taken >> i) & 1u) && (v[i] > bv || (v[i] == bv && e < be))) {
+        bv = v[i];
+        be = e;
+      }
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+      const float ov = __shfl_xor(bv, m, 64);
+      const int oe = __shfl_xor(be, m, 64);
+      if (ov > bv || (ov == bv && oe < be)) {
+        bv = ov;
+        be = oe;
+      }
+    }
+    if ((be & 63) == lane) taken |= 1u << (be >> 6);
+    if (lane == k) mine = bv;
+    if (k == 0) sl0 = bv;
+    if (lane == 0) sel[(size_t)row * topk + k] = be;
+  }
+  // Sum in rank order (lane 0 adds the ranks one by one).
+  const float ex = lane < topk ? __expf(mine - sl0) : 0.f;
+  for (int k = 0; k < topk; ++k) sum += __shfl(ex, k, 64);
+  if (lane < topk) wts[(size_t)row * (topk + 1) + lane] = ex / sum;
+  if (lane == 0) {
+    const float s = shared_logit ? shared_logit[row] : lg[E];
+    wts[(size_t)row * (topk + 1) + topk] = Sigmoid(s);
+  }
+}
+
+// ---- grouping --------------------------------------------------------------------------
+
+struct GroupOut {
+  int* counts;     // [E]
+  int* offsets;    // [E + 1]
+  int* pairs;      // [n]  route index (row * topk + slot) in expert-major stable order
+  int* row_ids;    // [n]  pairs / topk
+  int* inv;        // [n]  position of route i in pairs (nullable)
+  int4* entries;   // GEMM row entries (nullable): shared chunks first, then per-expert chunks
+  int* n_entries;  // total entries
+  int chunk;       // rows per entry
+  int M, topk, E;
+};
+
+// Shared-expert entries [0, ceil(M / chunk)), then expert e's ceil(count / chunk) chunks,
+// in expert order.  nch_base[e]: exclusive prefix of per-expert chunk counts.
+__device__ void WriteEntries(const GroupOut& o, int e, int nch_base, int count, int offset) {
+  const int nsh = (o.M + o.chunk - 1) / o.chunk;
+  for (int c = 0; c * o.chunk < count; ++c)
+    o.entries[nsh + nch_base + c] = make_int4(e, offset + c * o.chunk, min(o.chunk, count - c * o.chunk), 0);
+}
+__device__ void WriteSharedEntries(const GroupOut& o, int t, int nt) {
+  const int nsh = (o.M + o.chunk - 1) / o.chunk;
+  const int base = o.M * o.topk;
+  for (int c = t; c < nsh; c += nt) o.entries[c] = make_int4(o.E, base + c * o.chunk, min(o.chunk, o.M - c * o.chunk), 0);
+}
+
+// Exclusive block scan of one int per thread (blockDim.x == 1024); returns the prefix,
+// *total gets the sum.
+__device__ int BlockExclusiveScan(int v, int* scratch, int* total) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  int x = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int y = __shfl_up(x, d, 64);
+    if (lane >= d) x += y;
+  }
+  if (lane == 63) scratch[w] = x;
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    const int nw = blockDim.x >> 6;
+    int s = threadIdx.x < nw ? scratch[threadIdx.x] : 0;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int y = __shfl_up(s, d, 64);
+      if ((int)threadIdx.x >= d) s += y;
+    }
+    if (threadIdx.x < nw) scratch[64 + threadIdx.x] = s;
+  }
+  __syncthreads();
+  const int before = (w ? scratch[64 + w - 1] : 0) + x - v;
+  *total = scratch[64 + (blockDim.x >> 6) - 1];
+  __syncthreads();
+  return before;
+}
+
+// Whole grouping in one 1024-thread workgroup (up to kSmallRoutes routes): thread e
+// scans the routes in order and appends its expert's routes, so ranks are stable by
+// construction.  ref/prefill_ref.py:37-45.
+__global__ void __launch_bounds__(1024) GroupSmallKernel(const int* __restrict__ sel, GroupOut o) {
+  __shared__ int s_sel[kSmallRoutes];
+  __shared__ int s_cnt[kMaxExperts];
+  __shared__ int s_scan[128];
+  const int n = o.M * o.topk;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) s_sel[i] = sel[i];
+  __syncthreads();
+  // Counts (one thread per expert, in route order).
+  for (int e = threadIdx.x; e < o.E; e += blockDim.x) {
+    int c = 0;
+    for (int i = 0; i < n; ++i) c += s_sel[i] == e;
+    s_cnt[e] = c;
+  }
+  __syncthreads();
+  int total = 0, ctotal = 0;
+  // Offsets and entry bases: E <= 1024 experts, one per thread.
+  const int e = threadIdx.x;
+  const int cnt = e < o.E ? s_cnt[e] : 0;
+  const int off = BlockExclusiveScan(cnt, s_scan, &total);
+  const int nch = o.entries ? (cnt + o.chunk - 1) / o.chunk : 0;
+  const int chb = BlockExclusiveScan(nch, s_scan, &ctotal);
+  if (e < o.E) {
+    o.counts[e] = cnt;
+    o.offsets[e] = off;
+    int p = off;
+    for (int i = 0; i < n && p < off + cnt; ++i)
+      if (s_sel[i] == e) {
+        o.pairs[p] = i;
+        o.row_ids[p] = i / o.topk;
+        if (o.inv) o.inv[i] = p;
+        ++p;
+      }
+    if (o.entries) WriteEntries(o, e, chb, cnt, off);
+  }
+  if (e == 0) o.offsets[o.E] = total;
+  if (o.entries) {
+    WriteSharedEntries(o, threadIdx.x, blockDim.x);
+    if (threadIdx.x == 0) *o.n_entries = (o.M + o.chunk - 1) / o.chunk + ctotal;
+  }
+}
+
+// Multi-workgroup grouping for long prefill chunks: per-tile histograms, one scan, and
+// a stable in-tile scatter.  Tiles hold 1024 routes.
+constexpr int kTile = 1024;
+
+__global__ void __launch_bounds__(1024) GroupCountKernel(const int* __restrict__ sel, int n, int E, int ntiles,
+                                                         int* __restrict__ tile_counts) {
+  __shared__ int h[kMaxExperts];
+  for (int e = threadIdx.x; e < E; e += blockDim.x) h[e] = 0;
+  __syncthreads();
+  const int i = blockIdx.x * kTile + threadIdx.x;
+  if (i < n) atomicAdd(&h[sel[i]], 1);  // counts only; never decides order
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += blockDim.x) tile_counts[(size_t)e * ntiles + blockIdx.x] = h[e];
+}
+
+// One workgroup: exclusive scan of tile_counts in (expert, tile) order -> tile bases,
+// counts, offsets and the GEMM entries.
+__global__ void __launch_bounds__(1024) GroupScanKernel(int* __restrict__ tile_counts, int ntiles, GroupOut o) {
+  __shared__ int s_scan[128];
+  __shared__ int s_cnt[kMaxExperts];
+  const int e = threadIdx.x;
+  int cnt = 0;
+  if (e < o.E)
+    for (int t = 0; t < ntiles; ++t) cnt += tile_counts[(size_t)e * ntiles + t];
+  int total = 0, ctotal = 0;
+  const int off = BlockExclusiveScan(cnt, s_scan, &total);
+  const int nch = o.entries ? (cnt + o.chunk - 1) / o.chunk : 0;
+  const int chb = BlockExclusiveScan(nch, s_scan, &ctotal);
+  if (e < o.E) {
+    s_cnt[e] = cnt;
+    o.counts[e] = cnt;
+    o.offsets[e] = off;
+    int run = off;
+    for (int t = 0; t < ntiles; ++t) {
+      const int c = tile_counts[(size_t)e * ntiles + t];
+      tile_counts[(size_t)e * ntiles + t] = run;
+      run += c;
+    }
+    if (o.entries) WriteEntries(o, e, chb, cnt, off);
+  }
+  if (e == 0) o.offsets[o.E] = total;
+  if (o.entries) {
+    WriteSharedEntries(o, threadIdx.x, blockDim.x);
+    if (threadIdx.x == 0) *o.n_entries = (o.M + o.chunk - 1) / o.chunk + ctotal;
+  }
+}
+
+__global__ void __launch_bounds__(1024) GroupScatterKernel(const int* __restrict__ sel, const int* __restrict__ tile_base,
+                                                           int ntiles, GroupOut o) {
+  __shared__ int s_sel[kTile];
+  const int n = o.M * o.topk;
+  const int t0 = blockIdx.x * kTile;
+  const int len = min(kTile, n - t0);
+  for (int i = threadIdx.x; i < len; i += blockDim.x) s_sel[i] = sel[t0 + i];
+  __syncthreads();
+  for (int e = threadIdx.x; e < o.E; e += blockDim.x) {
+    int p = tile_base[(size_t)e * ntiles + blockIdx.x];
+    for (int i = 0; i < len; ++i)
+      if (s_sel[i] == e) {
+        const int r = t0 + i;
+        o.pairs[p] = r;
+        o.row_ids[p] = r / o.topk;
+        if (o.inv) o.inv[r] = p;
+        ++p;
+      }
+  }
+}
+
+// ---- activation transforms of the experts ----------------------------------------------
+
+struct ExpertTables {
+  const MatPtr* gate;  // [E + 1], index E = shared expert
+  const MatPtr* up;
+  const MatPtr* down;
+};
+
+// Gate and up input transforms of every compact row (each matrix has its own suh):
+// RoundH(x * suh) -> WHT128 -> * norm -> fp16 in MFMA row order.  engine/layers/moe_rows.h:102-125.
+__global__ void __launch_bounds__(256) MoeInputKernel(const __half* __restrict__ x, const int* __restrict__ sel,
+                                                      const int* __restrict__ pairs, ExpertTables tb, int M, int topk,
+                                                      int E, int H, __half* __restrict__ xg, __half* __restrict__ xu) {
+  const int nb = H / 128;
+  const int P = M * topk + M;
+  const int item = (blockIdx.x * blockDim.x + threadIdx.x) >> 5;
+  if (item >= P * nb * 2) return;
+  const int mat = item & 1, blk = (item >> 1) % nb, p = (item >> 1) / nb;
+  const int j = threadIdx.x & 31;
+  int row, e;
+  if (p < M * topk) {
+    const int route = pairs[p];
+    row = route / topk;
+    e = sel[route];
+  } else {
+    row = p - M * topk;
+    e = E;
+  }
+  const __half* suh = (mat ? tb.up : tb.gate)[e].suh;
+  const int c0 = blk * 128 + 4 * j;
+  const __half* xr = x + (size_t)row * H + c0;
+  float v[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = RoundH(H2F(xr[i]) * H2F(suh[c0 + i]));
+  Wht128x4(v);
+  __half* d = (mat ? xu : xg) + (size_t)p * H + blk * 128;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int el = 4 * j + i;
+    d[(el & ~31) + PermPos32(el & 31)] = __float2half(v[i] * kHadNorm);
+  }
+}
+
+// Mid: gate and up output transforms (fp32), RoundH(RoundH(SiLU(g) * u) * suh_down),
+// WHT128, * norm -> fp16 down input in MFMA row order.  engine/layers/moe_rows.h:543-566.
+__global__ void __launch_bounds__(256) MoeMidKernel(const float* __restrict__ yg, const float* __restrict__ yu,
+                                                    const int* __restrict__ sel, const int* __restrict__ pairs,
+                                                    ExpertTables tb, int M, int topk, int E, int I,
+                                                    __half* __restrict__ xd) {
+  const int nb = I / 128;
+  const int P = M * topk + M;
+  const int item = (blockIdx.x * blockDim.x + threadIdx.x) >> 5;
+  if (item >= P * nb) return;
+  const int blk = item % nb, p = item / nb;
+  const int j = threadIdx.x & 31;
+  const int e = p < M * topk ? sel[pairs[p]] : E;
+  const int c0 = blk * 128 + 4 * j;
+  const float4 g4 = *reinterpret_cast<const float4*>(yg + (size_t)p * I + c0);
+  const float4 u4 = *reinterpret_cast<const float4*>(yu + (size_t)p * I + c0);
+  float g[4] = {0.f + g4.x, 0.f + g4.y, 0.f + g4.z, 0.f + g4.w};
+  float u[4] = {0.f + u4.x, 0.f + u4.y, 0.f + u4.z, 0.f + u4.w};
+  Wht128x4(g);
+  Wht128x4(u);
+  const __half* svg = tb.gate[e].svh;
+  const __half* svu = tb.up[e].svh;
+  const __half* sud = tb.down[e].suh;
+  float v[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float gv = g[i] * (kHadNorm * H2F(svg[c0 + i]));
+    const float uv = u[i] * (kHadNorm * H2F(svu[c0 + i]));
+    v[i] = RoundH(RoundH(SiLU(gv) * uv) * H2F(sud[c0 + i]));
+  }
+  Wht128x4(v);
+  __half* d = xd + (size_t)p * I + blk * 128;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int el = 4 * j + i;
+    d[(el & ~31) + PermPos32(el & 31)] = __float2half(v[i] * kHadNorm);
+  }
+}
+
+// Combine: per row and 128-block, slots 0..topk-1 in selection order then the shared
+// expert: y += w_k * (WHT(d_k) * (norm * svh_k)), fp32.  engine/layers/moe_rows.h:634-682.
+__global__ void __launch_bounds__(256) MoeCombineKernel(const float* __restrict__ yd, const int* __restrict__ sel,
+                                                        const float* __restrict__ wts, const int* __restrict__ inv,
+                                                        ExpertTables tb, int M, int topk, int E, int H,
+                                                        float* __restrict__ y) {
+  const int nb = H / 128;
+  const int item = (blockIdx.x * blockDim.x + threadIdx.x) >> 5;
+  if (item >= M * nb) return;
+  const int blk = item % nb, r = item / nb;
+  const int j = threadIdx.x & 31;
+  const int c0 = blk * 128 + 4 * j;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int k = 0; k <= topk; ++k) {
+    const int p = k < topk ? inv[r * topk + k] : M * topk + r;
+    const int e = k < topk ? sel[r * topk + k] : E;
+    const float w = wts[(size_t)r * (topk + 1) + k];
+    const float4 d4 = *reinterpret_cast<const float4*>(yd + (size_t)p * H + c0);
+    float v[4] = {0.f + d4.x, 0.f + d4.y, 0.f + d4.z, 0.f + d4.w};
+    Wht128x4(v);
+    const __half* sv = tb.down[e].svh;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] += w * (v[i] * (kHadNorm * H2F(sv[c0 + i])));
+  }
+  *reinterpret_cast<float4*>(y + (size_t)r * H + c0) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+}
+
+}  // namespace cx
+
+// ---- plan ----------------------------------------------------------------------------------
+
+struct cx_moe_plan {
+  int H, I, E, topk;
+  int k2_gu, cb_gu, k2_d, cb_d;      // routed experts
+  int k2_sgu, cb_sgu, k2_sd, cb_sd;  // shared expert
+  cx::MatPtr* d_tables;              // device: gate[E+1], up[E+1], down[E+1]
+  cx::ExpertTables tb;
+  hipEvent_t* trace;                 // caller's events (nullable), recorded between stages
+  int n_trace, trace_cursor;
+};
+
+namespace cx {
+
+struct MoeSizes {
+  int M, P, n, nsh, chunk, nrb, max_entries, ntiles;
+  bool small;
+  size_t off_sel, off_wts, off_counts, off_offsets, off_pairs, off_rows, off_inv, off_ent, off_nent, off_tiles;
+  size_t off_xg, off_xu, off_yg, off_yu, off_xd, off_yd, total;
+};
+
+MoeSizes PlanMoe(const cx_moe_plan* pl, int M, int mode) {
+  MoeSizes s{};
+  s.M = M;
+  s.n = M * pl->topk;
+  s.P = s.n + M;
+  const bool decode = mode == CX_MOE_DECODE || (mode == CX_MOE_AUTO && M <= 64);
+  s.nrb = decode ? 1 : 4;
+  s.chunk = 16 * s.nrb;
+  s.nsh = (M + s.chunk - 1) / s.chunk;
+  s.max_entries = s.nsh + std::min(pl->E, s.n) + s.n / s.chunk;
+  s.small = s.n <= kSmallRoutes;
+  s.ntiles = (s.n + kTile - 1) / kTile;
+  size_t o = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = o;
+    o += AlignUp(bytes, 256);
+    return at;
+  };
+  s.off_sel = take((size_t)s.n * 4);
+  s.off_wts = take((size_t)M * (pl->topk + 1) * 4);
+  s.off_counts = take((size_t)pl->E * 4);
+  s.off_offsets = take((size_t)(pl->E + 1) * 4);
+  s.off_pairs = take((size_t)s.n * 4);
+  s.off_rows = take((size_t)s.n * 4);
+  s.off_inv = take((size_t)s.n * 4);
+  s.off_ent = take((size_t)s.max_entries * 16);
+  s.off_nent = take(4);
+  s.off_tiles = take((size_t)pl->E * s.ntiles * 4);
+  s.off_xg = take((size_t)s.P * pl->H * 2);
+  s.off_xu = take((size_t)s.P * pl->H * 2);
+  s.off_yg = take((size_t)s.P * pl->I * 4);
+  s.off_yu = take((size_t)s.P * pl->I * 4);
+  s.off_xd = take((size_t)s.P * pl->I * 2);
+  s.off_yd = take((size_t)s.P * pl->H * 4);
+  s.total = o;
+  return s;
+}
+
+int LaunchGroup(const int* sel, GroupOut& o, int* tile_counts, int ntiles, hipStream_t s) {
+  const int n = o.M * o.topk;
+  if (n <= kSmallRoutes) {
+    hipLaunchKernelGGL(GroupSmallKernel, dim3(1), dim3(1024), 0, s, sel, o);
+  } else {
+    hipLaunchKernelGGL(GroupCountKernel, dim3(ntiles), dim3(1024), 0, s, sel, n, o.E, ntiles, tile_counts);
+    hipLaunchKernelGGL(GroupScanKernel, dim3(1), dim3(1024), 0, s, tile_counts, ntiles, o);
+    hipLaunchKernelGGL(GroupScatterKernel, dim3(ntiles), dim3(1024), 0, s, sel, tile_counts, ntiles, o);
+  }
+  return LaunchStatus();
+}
+
+// Expert GEMM over the device-built entries: shared-expert entries [0, nsh) and routed
+// entries [nsh, n_entries).  Routed and shared matrices with different rates go in
+// separate launches.
+bool LaunchExpertGemm(const cx_moe_plan* pl, const MoeSizes& sz, bool gate_up, const __half* xa, const __half* xb,
+                      float* ya, float* yb, const int4* ent, const int* nent, hipStream_t s) {
+  GemmArgs g{};
+  const int in = gate_up ? pl->H : pl->I, out = gate_up ? pl->I : pl->H;
+  g.A = in / 16;
+  g.ncp = out / 32;
+  g.S = 1;
+  g.entries = ent;
+  if (gate_up) {
+    g.plane[0] = GemmPlane{pl->tb.gate, xa, ya, in, out, 0};
+    g.plane[1] = GemmPlane{pl->tb.up, xb, yb, in, out, 0};
+  } else {
+    g.plane[0] = GemmPlane{pl->tb.down, xa, ya, in, out, 0};
+    g.plane[1] = g.plane[0];
+  }
+  const int ksw = gate_up ? 4 : 1;
+  const int planes = gate_up ? 2 : 1;
+  const int k2r = gate_up ? pl->k2_gu : pl->k2_d, cbr = gate_up ? pl->cb_gu : pl->cb_d;
+  const int k2s = gate_up ? pl->k2_sgu : pl->k2_sd, cbs = gate_up ? pl->cb_sgu : pl->cb_sd;
+  const int cpg = g.ncp / (4 / ksw);
+  if (k2r == k2s && cbr == cbs) {
+    g.n_entries = nent;
+    g.entry_base = 0;
+    return LaunchGemm(k2r, cbr, sz.nrb, ksw, 4, dim3(cpg, sz.max_entries, planes), g, s);
+  }
+  g.n_entries = nullptr;
+  g.n_entries_host = sz.nsh;
+  g.entry_base = 0;
+  if (!LaunchGemm(k2s, cbs, sz.nrb, ksw, 4, dim3(cpg, sz.nsh, planes), g, s)) return false;
+  g.n_entries = nent;
+  g.entry_base = sz.nsh;
+  return LaunchGemm(k2r, cbr, sz.nrb, ksw, 4, dim3(cpg, sz.max_entries - sz.nsh, planes), g, s);
+}
+
+int CheckExpertShapes(const cx_moe_expert& ex, int H, int I) {
+  int rc;
+  if ((rc = CheckMatrix(&ex.gate)) || (rc = CheckMatrix(&ex.up)) || (rc = CheckMatrix(&ex.down))) return rc;
+  if (ex.gate.in_features != H || ex.gate.out_features != I || ex.up.in_features != H || ex.up.out_features != I ||
+      ex.down.in_features != I || ex.down.out_features != H)
+    return CX_E_SHAPE;
+  if (ex.gate.k2 != ex.up.k2 || ex.gate.codebook != ex.up.codebook) return CX_E_UNSUPPORTED;
+  return CX_OK;
+}
+
+}  // namespace cx
+
+using namespace cx;
+
 extern "C" {
-int cx_moe_route(const float*, int32_t, int32_t, int32_t, int32_t, const float*, int32_t*, float*, cx_stream_t) {
-  return CX_E_UNSUPPORTED;
+
+int cx_moe_route(const float* logits, int32_t ld, int32_t M, int32_t E, int32_t topk, const float* shared_logit,
+                 int32_t* sel, float* wts, cx_stream_t stream) {
+  if (!logits || !sel || !wts) return CX_E_ARG;
+  if (M <= 0 || E <= 0 || E > kMaxExperts || topk <= 0 || topk > kMaxTopK || topk > E || topk > 64) return CX_E_SHAPE;
+  if (ld < E || (!shared_logit && ld < E + 1)) return CX_E_SHAPE;
+  hipLaunchKernelGGL(RouteKernel, dim3((M + 3) / 4), dim3(256), 0, (hipStream_t)stream, logits, ld, M, E, topk,
+                     shared_logit, sel, wts);
+  return LaunchStatus();
 }
-size_t cx_moe_group_workspace_size(int32_t, int32_t, int32_t) { return 0; }
-int cx_moe_group(const int32_t*, int32_t, int32_t, int32_t, int32_t*, int32_t*, int32_t*, int32_t*, void*, size_t,
-                 cx_stream_t) {
-  return CX_E_UNSUPPORTED;
+
+size_t cx_moe_group_workspace_size(int32_t M, int32_t E, int32_t topk) {
+  if (M <= 0 || E <= 0 || topk <= 0) return 0;
+  const int n = M * topk;
+  return AlignUp((size_t)E * ((n + kTile - 1) / kTile) * 4, 256);
 }
-int cx_moe_plan_create(const cx_moe_layer*, cx_moe_plan**) { return CX_E_UNSUPPORTED; }
-void cx_moe_plan_destroy(cx_moe_plan*) {}
-size_t cx_moe_layer_workspace_size(const cx_moe_plan*, int32_t, int32_t) { return 0; }
-int cx_moe_layer_forward(const cx_moe_plan*, const uint16_t*, const float*, int32_t, const float*, int32_t,
-                         const int32_t*, int32_t, float*, int32_t*, float*, int32_t, void*, size_t, cx_stream_t) {
-  return CX_E_UNSUPPORTED;
+
+int cx_moe_group(const int32_t* sel, int32_t M, int32_t E, int32_t topk, int32_t* counts, int32_t* offsets,
+                 int32_t* pairs, int32_t* row_ids, void* workspace, size_t workspace_bytes, cx_stream_t stream) {
+  if (!sel || !counts || !offsets || !pairs || !row_ids) return CX_E_ARG;
+  if (M <= 0 || E <= 0 || E > kMaxExperts || topk <= 0 || topk > E) return CX_E_SHAPE;
+  const int n = M * topk;
+  const int ntiles = (n + kTile - 1) / kTile;
+  if (n > kSmallRoutes && (!workspace || workspace_bytes < cx_moe_group_workspace_size(M, E, topk)))
+    return CX_E_WORKSPACE;
+  GroupOut o{counts, offsets, pairs, row_ids, nullptr, nullptr, nullptr, 16, M, topk, E};
+  return LaunchGroup(sel, o, static_cast<int*>(workspace), ntiles, (hipStream_t)stream);
 }
+
+int cx_moe_plan_create(const cx_moe_layer* layer, cx_moe_plan** out) {
+  if (!layer || !out || !layer->experts) return CX_E_ARG;
+  *out = nullptr;
+  const int H = layer->hidden, I = layer->intermediate, E = layer->n_experts;
+  if (H <= 0 || I <= 0 || H % 128 || I % 128) return CX_E_SHAPE;
+  if (E <= 0 || E > kMaxExperts || layer->topk <= 0 || layer->topk > E || layer->topk > kMaxTopK) return CX_E_SHAPE;
+  int rc;
+  for (int e = 0; e < E; ++e) {
+    if ((rc = CheckExpertShapes(layer->experts[e], H, I))) return rc;
+    const cx_moe_expert& a = layer->experts[e];
+    const cx_moe_expert& b = layer->experts[0];
+    if (a.gate.k2 != b.gate.k2 || a.gate.codebook != b.gate.codebook || a.down.k2 != b.down.k2 ||
+        a.down.codebook != b.down.codebook)
+      return CX_E_UNSUPPORTED;
+  }
+  if ((rc = CheckExpertShapes(layer->shared, H, I))) return rc;
+  cx_moe_plan* pl = new (std::nothrow) cx_moe_plan{};
+  if (!pl) return CX_E_ARG;
+  pl->H = H;
+  pl->I = I;
+  pl->E = E;
+  pl->topk = layer->topk;
+  pl->k2_gu = layer->experts[0].gate.k2;
+  pl->cb_gu = layer->experts[0].gate.codebook;
+  pl->k2_d = layer->experts[0].down.k2;
+  pl->cb_d = layer->experts[0].down.codebook;
+  pl->k2_sgu = layer->shared.gate.k2;
+  pl->cb_sgu = layer->shared.gate.codebook;
+  pl->k2_sd = layer->shared.down.k2;
+  pl->cb_sd = layer->shared.down.codebook;
+  const size_t n = (size_t)(E + 1);
+  MatPtr* host = static_cast<MatPtr*>(std::malloc(sizeof(MatPtr) * 3 * n));
+  if (!host) {
+    delete pl;
+    return CX_E_ARG;
+  }
+  auto mp = [](const cx_exl3_matrix& m) {
+    return MatPtr{m.tiles, reinterpret_cast<const __half*>(m.suh), reinterpret_cast<const __half*>(m.svh)};
+  };
+  for (int e = 0; e <= E; ++e) {
+    const cx_moe_expert& ex = e < E ? layer->experts[e] : layer->shared;
+    host[e] = mp(ex.gate);
+    host[n + e] = mp(ex.up);
+    host[2 * n + e] = mp(ex.down);
+  }
+  hipError_t err = hipMalloc(&pl->d_tables, sizeof(MatPtr) * 3 * n);
+  if (err == hipSuccess) err = hipMemcpy(pl->d_tables, host, sizeof(MatPtr) * 3 * n, hipMemcpyHostToDevice);
+  std::free(host);
+  if (err != hipSuccess) {
+    if (pl->d_tables) (void)hipFree(pl->d_tables);
+    delete pl;
+    return (int)err;
+  }
+  pl->tb = ExpertTables{pl->d_tables, pl->d_tables + n, pl->d_tables + 2 * n};
+  *out = pl;
+  return CX_OK;
 }
+
+void cx_moe_plan_destroy(cx_moe_plan* plan) {
+  if (!plan) return;
+  if (plan->d_tables) (void)hipFree(plan->d_tables);
+  std::free(plan->trace);
+  delete plan;
+}
+
+size_t cx_moe_layer_workspace_size(const cx_moe_plan* plan, int32_t M, int32_t mode) {
+  if (!plan || M <= 0) return 0;
+  return PlanMoe(plan, M, mode).total;
+}
+
+int cx_moe_layer_forward(const cx_moe_plan* pl, const uint16_t* x, const float* logits, int32_t ld,
+                         const float* shared_logit, int32_t M, const int32_t* row_offsets, int32_t n_sessions, float* y,
+                         int32_t* sel_out, float* wts_out, int32_t mode, void* workspace, size_t workspace_bytes,
+                         cx_stream_t stream) {
+  if (!pl || !x || !logits || !y || !workspace) return CX_E_ARG;
+  if (mode < CX_MOE_AUTO || mode > CX_MOE_PREFILL) return CX_E_ARG;
+  if (M <= 0) return CX_E_SHAPE;
+  if (ld < pl->E || (!shared_logit && ld < pl->E + 1)) return CX_E_SHAPE;
+  int rc;
+  if ((rc = RowOffsetsCheck(row_offsets, n_sessions, M))) return rc;
+  const MoeSizes sz = PlanMoe(pl, M, mode);
+  if (workspace_bytes < sz.total) return CX_E_WORKSPACE;
+  hipStream_t s = (hipStream_t)stream;
+  char* ws = static_cast<char*>(workspace);
+  int* sel = sel_out ? sel_out : reinterpret_cast<int*>(ws + sz.off_sel);
+  float* wts = wts_out ? wts_out : reinterpret_cast<float*>(ws + sz.off_wts);
+  int* counts = reinterpret_cast<int*>(ws + sz.off_counts);
+  int* offsets = reinterpret_cast<int*>(ws + sz.off_offsets);
+  int* pairs = reinterpret_cast<int*>(ws + sz.off_pairs);
+  int* rows = reinterpret_cast<int*>(ws + sz.off_rows);
+  int* inv = reinterpret_cast<int*>(ws + sz.off_inv);
+  int4* ent = reinterpret_cast<int4*>(ws + sz.off_ent);
+  int* nent = reinterpret_cast<int*>(ws + sz.off_nent);
+  int* tiles = reinterpret_cast<int*>(ws + sz.off_tiles);
+  __half* xg = reinterpret_cast<__half*>(ws + sz.off_xg);
+  __half* xu = reinterpret_cast<__half*>(ws + sz.off_xu);
+  float* yg = reinterpret_cast<float*>(ws + sz.off_yg);
+  float* yu = reinterpret_cast<float*>(ws + sz.off_yu);
+  __half* xd = reinterpret_cast<__half*>(ws + sz.off_xd);
+  float* yd = reinterpret_cast<float*>(ws + sz.off_yd);
+
+  cx_moe_plan* mp = const_cast<cx_moe_plan*>(pl);
+  auto mark = [&]() {
+    if (mp->trace && mp->n_trace > 0) {
+      (void)hipEventRecord(mp->trace[mp->trace_cursor], s);
+      mp->trace_cursor = (mp->trace_cursor + 1) % mp->n_trace;
+    }
+  };
+  mark();
+  hipLaunchKernelGGL(RouteKernel, dim3((M + 3) / 4), dim3(256), 0, s, logits, ld, M, pl->E, pl->topk, shared_logit,
+                     sel, wts);
+  mark();
+  GroupOut o{counts, offsets, pairs, rows, inv, ent, nent, sz.chunk, M, pl->topk, pl->E};
+  if ((rc = LaunchGroup(sel, o, tiles, sz.ntiles, s))) return rc;
+  mark();
+  {
+    const long items = (long)sz.P * (pl->H / 128) * 2;
+    hipLaunchKernelGGL(MoeInputKernel, dim3((unsigned)((items * 32 + 255) / 256)), dim3(256), 0, s,
+                       reinterpret_cast<const __half*>(x), sel, pairs, pl->tb, M, pl->topk, pl->E, pl->H, xg, xu);
+  }
+  mark();
+  if (!LaunchExpertGemm(pl, sz, true, xg, xu, yg, yu, ent, nent, s)) return CX_E_UNSUPPORTED;
+  mark();
+  {
+    const long items = (long)sz.P * (pl->I / 128);
+    hipLaunchKernelGGL(MoeMidKernel, dim3((unsigned)((items * 32 + 255) / 256)), dim3(256), 0, s, yg, yu, sel, pairs,
+                       pl->tb, M, pl->topk, pl->E, pl->I, xd);
+  }
+  mark();
+  if (!LaunchExpertGemm(pl, sz, false, xd, nullptr, yd, nullptr, ent, nent, s)) return CX_E_UNSUPPORTED;
+  mark();
+  {
+    const long items = (long)M * (pl->H / 128);
+    hipLaunchKernelGGL(MoeCombineKernel, dim3((unsigned)((items * 32 + 255) / 256)), dim3(256), 0, s, yd, sel, wts,
+                       inv, pl->tb, M, pl->topk, pl->E, pl->H, y);
+  }
+  mark();
+  return LaunchStatus();
+}
+
+int cx_moe_plan_set_trace(cx_moe_plan* plan, void* const* events, int32_t n_events) {
+  if (!plan || n_events < 0 || (n_events > 0 && !events)) return CX_E_ARG;
+  std::free(plan->trace);
+  plan->trace = nullptr;
+  plan->n_trace = 0;
+  plan->trace_cursor = 0;
+  if (n_events == 0) return CX_OK;
+  plan->trace = static_cast<hipEvent_t*>(std::malloc(sizeof(hipEvent_t) * n_events));
+  if (!plan->trace) return CX_E_ARG;
+  for (int i = 0; i < n_events; ++i) plan->trace[i] = static_cast<hipEvent_t>(events[i]);
+  plan->n_trace = n_events;
+  return CX_OK;
+}
+
+}  // extern "C"

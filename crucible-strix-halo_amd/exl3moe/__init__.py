@@ -22,7 +22,7 @@ ERRORS = {-1: "invalid argument", -2: "invalid shape", -3: "unsupported bitrate"
 EXPORTED = [
     "cx_exl3_tile_bytes", "cx_exl3_repack", "cx_exl3_dequant", "cx_exl3_linear_workspace_size", "cx_exl3_linear",
     "cx_moe_route", "cx_moe_group_workspace_size", "cx_moe_group", "cx_moe_plan_create", "cx_moe_plan_destroy",
-    "cx_moe_layer_workspace_size", "cx_moe_layer_forward", "cx_version",
+    "cx_moe_layer_workspace_size", "cx_moe_layer_forward", "cx_moe_plan_set_trace", "cx_version",
 ]
 
 
@@ -74,6 +74,8 @@ def lib() -> ctypes.CDLL:
         L.cx_moe_layer_workspace_size.argtypes = [P, I32, I32]
         L.cx_moe_layer_workspace_size.restype = SZ
         L.cx_moe_layer_forward.argtypes = [P, P, P, I32, P, I32, P, I32, P, P, P, I32, P, SZ, P]
+        L.cx_moe_plan_set_trace.argtypes = [P, ctypes.POINTER(ctypes.c_void_p), I32]
+        L.cx_moe_plan_set_trace.restype = ctypes.c_int
         L.cx_version.restype = ctypes.c_char_p
         for fn in ("cx_exl3_repack", "cx_exl3_dequant", "cx_exl3_linear", "cx_moe_route", "cx_moe_group",
                    "cx_moe_plan_create", "cx_moe_layer_forward"):

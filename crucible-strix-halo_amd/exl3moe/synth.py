@@ -26,9 +26,44 @@ def sessions(rng, n: int, lo: int, hi: int) -> list[int]:
     return [0] + np.cumsum(sizes).tolist()
 
 
-def zipf_bias(rng, E: int, s: float = 1.1, scale: float = 3.0) -> np.ndarray:
+def zipf_bias(rng, E: int, s: float = 1.1, scale: float = 0.23) -> np.ndarray:
     """Per-expert router bias from Zipf(s) rank weights (a random expert order), scaled so
-    expert token counts are skewed (a few hundred tokens on the heaviest experts)."""
+    expert token counts are skewed: at 2048 tokens and top-10 the heaviest expert gets
+    about 400 tokens and the lightest about 10."""
     ranks = rng.permutation(E) + 1
     w = ranks.astype(np.float64) ** (-s)
     return (scale * np.log(w / w.mean())).astype(np.float32)
+
+
+def device_linear(gen, I: int, O: int, bits: float, device="cuda", codebook: str = "mul1"):
+    """A random EXL3 linear generated on the device (checkpoint-order trellis kept for
+    host-side checks), repacked into the library layout."""
+    import torch
+    from .ops import DeviceLinear
+    k2 = int(round(bits * 2))
+    tr = torch.randint(-32768, 32768, (I // 16, O // 16, 8 * k2), dtype=torch.int16, device=device, generator=gen)
+    suh = (torch.randint(0, 2, (I,), device=device, generator=gen) * 2 - 1).to(torch.float16)
+    sign = torch.randint(0, 2, (O,), device=device, generator=gen) * 2 - 1
+    svh = ((torch.rand(O, device=device, generator=gen) + 0.5) * sign).to(torch.float16)
+    lin = DeviceLinear.from_trellis(tr, suh, svh, bits, codebook)
+    lin.trellis = tr
+    return lin
+
+
+def device_moe_layer(seed: int, E: int, H: int, Ie: int, topk: int, bits_gu: float = 4, bits_d: float = 4,
+                     shared_bits_gu: float | None = None, shared_bits_d: float | None = None, device="cuda"):
+    """Seeded synthetic MoE layer on the device: E routed experts plus the shared expert."""
+    import torch
+    from .ops import MoePlan
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    sg = bits_gu if shared_bits_gu is None else shared_bits_gu
+    sd = bits_d if shared_bits_d is None else shared_bits_d
+
+    def one(bgu, bd):
+        return {"gate": device_linear(gen, H, Ie, bgu, device), "up": device_linear(gen, H, Ie, bgu, device),
+                "down": device_linear(gen, Ie, H, bd, device)}
+
+    experts = [one(bits_gu, bits_d) for _ in range(E)]
+    shared = one(sg, sd)
+    return MoePlan(H, Ie, experts, shared, topk)

@@ -138,6 +138,15 @@ int cx_moe_layer_forward(const cx_moe_plan* plan, const uint16_t* x, const float
                  const float* shared_logit, int32_t M, const int32_t* row_offsets, int32_t n_sessions, float* y,
                  int32_t* sel, float* wts, int32_t mode, void* workspace, size_t workspace_bytes, cx_stream_t stream);
 
+/* Stage tracing (the reference's per-stage hipEvent marks, engine/engine.hip:2086-2095,
+ * stages named at engine/engine.hip:1349-1363).  With n_events > 0 every
+ * cx_moe_layer_forward records CX_MOE_TRACE_MARKS events on its stream, into the caller's
+ * hipEvent_t array used as a ring: mark 0 before the router, then one after each stage:
+ * route, group, input transform, gate/up GEMM, mid, down GEMM, combine.  The plan keeps a
+ * copy of the handles; n_events = 0 turns tracing off. */
+#define CX_MOE_TRACE_MARKS 8
+int cx_moe_plan_set_trace(cx_moe_plan* plan, void* const* events, int32_t n_events);
+
 /* Library version string. */
 const char* cx_version(void);
 
