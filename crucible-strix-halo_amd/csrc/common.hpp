@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <type_traits>
 
 namespace cx {
 
@@ -43,6 +44,80 @@ __device__ __forceinline__ void Wht128x4(float v[4]) {
   }
 }
 
+// ---- cross-lane moves inside 16-lane rows (DPP, plain VALU: no LDS traffic) ----------
+template <int CTRL>
+__device__ __forceinline__ float Dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int DppI(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
+}
+constexpr int kDppQuadSwap1 = 0xB1;     // quad_perm [1,0,3,2]: lane ^ 1
+constexpr int kDppQuadSwap2 = 0x4E;     // quad_perm [2,3,0,1]: lane ^ 2
+constexpr int kDppQuadReverse = 0x1B;   // quad_perm [3,2,1,0]: lane ^ 3
+constexpr int kDppRowMirror = 0x140;    // lane 15 - i within 16
+constexpr int kDppRowHalfMirror = 0x141;  // lane 7 - i within 8 (lane ^ 7)
+// Value of lane ^ M (M = 1, 2, 4, 8) within each 16-lane row.
+template <int M>
+__device__ __forceinline__ float XorLane(float v) {
+  if constexpr (M == 1) return Dpp<kDppQuadSwap1>(v);
+  else if constexpr (M == 2) return Dpp<kDppQuadSwap2>(v);
+  else if constexpr (M == 4) return Dpp<kDppQuadReverse>(Dpp<kDppRowHalfMirror>(v));  // (i ^ 7) ^ 3
+  else return Dpp<kDppRowHalfMirror>(Dpp<kDppRowMirror>(v));                          // (i ^ 15) ^ 7
+}
+
+// 128-point natural-order Sylvester butterfly, 16 lanes per block (a wave64 holds four
+// blocks, one per 16-lane row).  Lane j of a block holds elements 8j..8j+7.  Strides
+// 1, 2, 4 are in-lane, strides 8..64 are lane xors 1..8 by DPP, in increasing order; each
+// output is lo + hi or lo - hi of the same two fp32 operands, so the values are those of
+// any evaluation of the same butterfly network.  All 64 lanes must be active.
+__device__ __forceinline__ void Wht128x8(float v[8]) {
+#pragma unroll
+  for (int st = 1; st < 8; st <<= 1)
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (!(i & st)) {
+        const float lo = v[i], hi = v[i + st];
+        v[i] = lo + hi;
+        v[i + st] = lo - hi;
+      }
+  const int j = threadIdx.x & 15;
+  auto stage = [&](auto mc) {
+    constexpr int M = decltype(mc)::value;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float o = XorLane<M>(v[i]);
+      v[i] = (j & M) ? (o - v[i]) : (v[i] + o);
+    }
+  };
+  stage(std::integral_constant<int, 1>{});
+  stage(std::integral_constant<int, 2>{});
+  stage(std::integral_constant<int, 4>{});
+  stage(std::integral_constant<int, 8>{});
+}
+
+// Wave-uniform max / min by DPP row reductions and four lane reads.
+__device__ __forceinline__ float WaveMaxF(float v) {
+  v = fmaxf(v, Dpp<kDppQuadSwap1>(v));
+  v = fmaxf(v, Dpp<kDppQuadSwap2>(v));
+  v = fmaxf(v, Dpp<kDppRowHalfMirror>(v));
+  v = fmaxf(v, Dpp<kDppRowMirror>(v));
+  const float a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+  const float b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+  const float c = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+  const float d = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+  return fmaxf(fmaxf(a, b), fmaxf(c, d));
+}
+__device__ __forceinline__ int WaveMinI(int v) {
+  v = min(v, DppI<kDppQuadSwap1>(v));
+  v = min(v, DppI<kDppQuadSwap2>(v));
+  v = min(v, DppI<kDppRowHalfMirror>(v));
+  v = min(v, DppI<kDppRowMirror>(v));
+  return min(min(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+             min(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+}
+
 // Position of input row r (0..15 of a 16-row block) in the MFMA-ordered activation
 // layout.  Lane group q of a 16x16x16 MFMA feeds rows {2q, 2q+1, 2q+8, 2q+9} of a
 // weight tile (the decoder's run layout), so activations are stored as
@@ -54,6 +129,38 @@ __host__ __device__ constexpr int PermRow16(int p) { return 2 * (p >> 2) + (p & 
 __host__ __device__ constexpr int PermPos32(int r) { return 8 * ((r & 7) >> 1) + 4 * (r >> 4) + (r & 1) + 2 * ((r >> 3) & 1); }
 __host__ __device__ constexpr int PermRow32(int p) {
   return 16 * ((p >> 2) & 1) + 2 * (p >> 3) + (p & 1) + 8 * ((p >> 1) & 1);
+}
+
+// Stores 8 fp16 values of elements 8j..8j+7 of a 128-block (j = lane & 15) in the
+// 32-row MFMA order: element 8j + i goes to 32 (j >> 2) + PermPos32(8 (j & 3) + i), i.e.
+// pairs (i, i + 1) land in adjacent halves.  d: the block's first half.
+__device__ __forceinline__ void StorePerm32x8(__half* d, const float v[8], float scale) {
+  const int j = threadIdx.x & 15;
+  const int base = 32 * (j >> 2) + 4 * ((j >> 1) & 1) + 2 * (j & 1);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const __half2 h = __floats2half2_rn(v[2 * k] * scale, v[2 * k + 1] * scale);
+    *reinterpret_cast<__half2*>(d + base + 8 * k) = h;
+  }
+}
+__device__ __forceinline__ void LoadH8(const __half* p, float v[8]) {
+  const uint4 u = *reinterpret_cast<const uint4*>(p);
+  const __half2* h = reinterpret_cast<const __half2*>(&u);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const float2 f = __half22float2(h[k]);
+    v[2 * k] = f.x;
+    v[2 * k + 1] = f.y;
+  }
+}
+__device__ __forceinline__ void LoadF8(const float* p, float v[8]) {
+  const float4 a = *reinterpret_cast<const float4*>(p), b = *reinterpret_cast<const float4*>(p + 4);
+  v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+  v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+__device__ __forceinline__ void StoreF8(float* p, const float v[8]) {
+  *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+  *reinterpret_cast<float4*>(p + 4) = make_float4(v[4], v[5], v[6], v[7]);
 }
 
 // Raw buffer resource over [base, base + bytes): loads past the end return zero.

@@ -56,28 +56,23 @@ __global__ void __launch_bounds__(256) DequantKernel(const uint32_t* __restrict_
 // ---- activation transforms ----------------------------------------------------------
 
 // Input transform of fp16 rows: RoundH(x * suh) -> WHT128 -> * norm -> fp16, stored in
-// MFMA row order.  One 128-block per 32 lanes.  rows[i] (nullable) maps output row i to
-// its input row.  ref/exl3_ref.py:140-152; engine/exl3/exl3.h:48-65.
+// MFMA row order.  One 128-block per 16 lanes.  ref/exl3_ref.py:140-152;
+// engine/exl3/exl3.h:48-65.
 __global__ void __launch_bounds__(256) InputTransformKernel(const __half* __restrict__ x, int ldx,
-                                                            const int* __restrict__ rows, const __half* __restrict__ suh,
-                                                            __half* __restrict__ xp, int M, int I) {
+                                                            const __half* __restrict__ suh, __half* __restrict__ xp,
+                                                            int M, int I) {
   const int nb = I / 128;
-  const int item = (blockIdx.x * blockDim.x + threadIdx.x) >> 5;
+  const int item = (blockIdx.x * blockDim.x + threadIdx.x) >> 4;
   if (item >= M * nb) return;
-  const int r = item / nb, blk = item % nb, j = threadIdx.x & 31;
-  const int src = rows ? rows[r] : r;
-  const int c0 = blk * 128 + 4 * j;
-  const __half* xr = x + (size_t)src * ldx + c0;
-  float v[4];
+  const int r = item / nb, blk = item % nb, j = threadIdx.x & 15;
+  const int c0 = blk * 128 + 8 * j;
+  float v[8], s[8];
+  LoadH8(x + (size_t)r * ldx + c0, v);
+  LoadH8(suh + c0, s);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) v[i] = RoundH(H2F(xr[i]) * H2F(suh[c0 + i]));
-  Wht128x4(v);
-  __half* d = xp + (size_t)r * I + blk * 128;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int e = 4 * j + i;
-    d[(e & ~31) + PermPos32(e & 31)] = __float2half(v[i] * kHadNorm);
-  }
+  for (int i = 0; i < 8; ++i) v[i] = RoundH(v[i] * s[i]);
+  Wht128x8(v);
+  StorePerm32x8(xp + (size_t)r * I + blk * 128, v, kHadNorm);
 }
 
 // Fixed-order sum of S K-segment partials, then the output transform.
@@ -87,31 +82,30 @@ __global__ void __launch_bounds__(256) OutputTransformKernel(const float* __rest
                                                              int S, const __half* __restrict__ svh, void* y, int M,
                                                              int O, int f16) {
   const int nb = O / 128;
-  const int item = (blockIdx.x * blockDim.x + threadIdx.x) >> 5;
+  const int item = (blockIdx.x * blockDim.x + threadIdx.x) >> 4;
   if (item >= M * nb) return;
-  const int r = item / nb, blk = item % nb, j = threadIdx.x & 31;
-  const int c0 = blk * 128 + 4 * j;
-  float v[4] = {0.f, 0.f, 0.f, 0.f};
+  const int r = item / nb, blk = item % nb, j = threadIdx.x & 15;
+  const int c0 = blk * 128 + 8 * j;
+  float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, p[8], sv[8];
   for (int s = 0; s < S; ++s) {
-    const float4 p = *reinterpret_cast<const float4*>(part + s * seg_stride + (size_t)r * O + c0);
-    v[0] += p.x;
-    v[1] += p.y;
-    v[2] += p.z;
-    v[3] += p.w;
+    LoadF8(part + s * seg_stride + (size_t)r * O + c0, p);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] += p[i];
   }
   if (f16) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = RoundH(v[i]);
+    for (int i = 0; i < 8; ++i) v[i] = RoundH(v[i]);
   }
-  Wht128x4(v);
+  Wht128x8(v);
+  LoadH8(svh + c0, sv);
   if (f16) {
     __half* d = reinterpret_cast<__half*>(y) + (size_t)r * O + c0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) d[i] = __float2half(RoundH(v[i] * kHadNorm) * H2F(svh[c0 + i]));
+    for (int i = 0; i < 8; ++i) d[i] = __float2half(RoundH(v[i] * kHadNorm) * sv[i]);
   } else {
-    float* d = reinterpret_cast<float*>(y) + (size_t)r * O + c0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) d[i] = v[i] * (kHadNorm * H2F(svh[c0 + i]));
+    for (int i = 0; i < 8; ++i) v[i] *= kHadNorm * sv[i];
+    StoreF8(reinterpret_cast<float*>(y) + (size_t)r * O + c0, v);
   }
 }
 
@@ -267,12 +261,11 @@ int cx_exl3_linear(const cx_exl3_matrix* m, const uint16_t* x, int32_t M, const 
   FillLinearTables(ent, mat, p, M, m, s);
   {
     const int items = M * (I / 128);
-    hipLaunchKernelGGL(InputTransformKernel, dim3((items * 32 + 255) / 256), dim3(256), 0, s,
-                       reinterpret_cast<const __half*>(x), I, (const int*)nullptr,
-                       reinterpret_cast<const __half*>(m->suh), xp, M, I);
+    hipLaunchKernelGGL(InputTransformKernel, dim3((items * 16 + 255) / 256), dim3(256), 0, s,
+                       reinterpret_cast<const __half*>(x), I, reinterpret_cast<const __half*>(m->suh), xp, M, I);
   }
   GemmArgs g{};
-  g.plane[0] = GemmPlane{mat, xp, part, I, O, (long long)M * O};
+  g.plane[0] = GemmPlane{mat, xp, part, I, O, (long long)M * O, 0};
   g.plane[1] = g.plane[0];
   g.entries = ent;
   g.n_entries = nullptr;
@@ -284,7 +277,7 @@ int cx_exl3_linear(const cx_exl3_matrix* m, const uint16_t* x, int32_t M, const 
   if (!LaunchGemm(m->k2, m->codebook, p.nrb, p.ksw, p.u, grid, g, s)) return CX_E_UNSUPPORTED;
   {
     const int items = M * (O / 128);
-    hipLaunchKernelGGL(OutputTransformKernel, dim3((items * 32 + 255) / 256), dim3(256), 0, s, part,
+    hipLaunchKernelGGL(OutputTransformKernel, dim3((items * 16 + 255) / 256), dim3(256), 0, s, part,
                        (long long)M * O, p.S, reinterpret_cast<const __half*>(m->svh), y, M, O,
                        y_dtype == CX_F16 ? 1 : 0);
   }

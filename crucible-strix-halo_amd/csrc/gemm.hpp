@@ -34,9 +34,10 @@ struct MatPtr {
 struct GemmPlane {
   const MatPtr* mats;  // indexed by the entry's matrix id
   const __half* x;     // MFMA-ordered activations; row r at x + r * ldx
-  float* y;            // fp32 raw outputs; row r at y + r * ldy (+ K segment * seg_stride)
+  float* y;            // fp32 outputs; row r at y + r * ldy (+ K segment * seg_stride)
   int ldx, ldy;
   long long seg_stride;
+  int epi;  // 0: raw sums y_h; 1: output transform WHT128(y_h) * norm * svh (needs KSW = 1, S = 1)
 };
 
 struct GemmArgs {
@@ -178,6 +179,37 @@ __global__ void __launch_bounds__(256) Exl3GemmKernel(GemmArgs g) {
         acc[rb][0] += red[c][k][rb * 2][lane];
         acc[rb][1] += red[c][k][rb * 2 + 1][lane];
       }
+  }
+  if constexpr (KSW == 1) {
+    if (pl.epi == 1) {
+      // The workgroup holds columns [128 cpg, 128 cpg + 128): one whole output Hadamard
+      // block.  Stage y_h in LDS, then WHT128 * norm * svh per row (engine LinOutBlock,
+      // engine/exl3/exl3.h:69-82), fp32.
+      __shared__ float ebuf[16 * NRB][132];
+      const int cl = wave * 32 + ((lane & 15) >> 3) * 16 + (lane & 7);
+#pragma unroll
+      for (int rb = 0; rb < NRB; ++rb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = rb * 16 + 4 * (lane >> 4) + i;
+          ebuf[r][cl] = acc[rb][0][i];
+          ebuf[r][cl + 8] = acc[rb][1][i];
+        }
+      __syncthreads();
+      const int j = threadIdx.x & 15, c0 = cpg * 128 + 8 * j;
+      float sv[8];
+      LoadH8(m.svh + c0, sv);
+      for (int r = threadIdx.x >> 4; r < nrows; r += 16) {
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = 0.f + ebuf[r][8 * j + i];
+        Wht128x8(v);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] *= kHadNorm * sv[i];
+        StoreF8(pl.y + (size_t)(row0 + r) * pl.ldy + c0, v);
+      }
+      return;
+    }
   }
   float* y = pl.y + (size_t)kseg * pl.seg_stride;
   const int col = (2 * cp + ((lane & 15) >> 3)) * 16 + (lane & 7);

@@ -21,59 +21,47 @@ constexpr int kSmallRoutes = 2048;  // single-workgroup grouping up to this many
 // ---- router ---------------------------------------------------------------------------
 
 // One wave per row: top-k of E logits by repeated wave argmax (logit descending, lower
-// id on ties), then the selection softmax exp(l_k - l_0) / sum_j exp(l_j - l_0) summed in
-// rank order, and sigmoid of the shared logit.  engine/layers/ops.h:683-713.
+// id on ties) with DPP reductions, then the selection softmax exp(l_k - l_0) /
+// sum_j exp(l_j - l_0) summed in rank order, and sigmoid of the shared logit.
+// engine/layers/ops.h:683-713.  V = logits per lane (E <= 64 V).
+template <int V>
 __global__ void __launch_bounds__(256) RouteKernel(const float* __restrict__ logits, int ld, int M, int E, int topk,
                                                    const float* __restrict__ shared_logit, int* __restrict__ sel,
                                                    float* __restrict__ wts) {
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= M) return;
+  if (row >= M) return;  // whole waves leave together
   const int lane = threadIdx.x & 63;
   const float* lg = logits + (size_t)row * ld;
-  constexpr int V = kMaxExperts / 64;
   float v[V];
 #pragma unroll
   for (int i = 0; i < V; ++i) {
     const int e = i * 64 + lane;
     v[i] = e < E ? lg[e] : -INFINITY;
   }
-  unsigned taken = 0;  // bit i: this lane's value i is already selected
-  float sl0 = 0.f, sum = 0.f;
-  float mine = 0.f;  // lane k < topk keeps the logit of rank k
+  float mine = 0.f, top = 0.f;  // lane k < topk keeps the logit of rank k
+  unsigned taken = 0;            // bit i: this lane's logit i is selected
   for (int k = 0; k < topk; ++k) {
-    // Lane-local best among values not taken: value desc, id asc.
+    // Lane-local best (value desc, id asc); ids of a lane increase with i.
     float bv = -INFINITY;
-    int be = 0x7fffffff;
+    int bi = V;
 #pragma unroll
-    for (int i = 0; i < V; ++i) {
-      const int e = i * 64 + lane;
-      if (e < E && !((taken >> i) & 1u) && (v[i] > bv || (v[i] == bv && e < be))) {
+    for (int i = V - 1; i >= 0; --i)
+      if (v[i] >= bv && i * 64 + lane < E && !((taken >> i) & 1u)) {
         bv = v[i];
-        be = e;
+        bi = i;
       }
-    }
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-      const float ov = __shfl_xor(bv, m, 64);
-      const int oe = __shfl_xor(be, m, 64);
-      if (ov > bv || (ov == bv && oe < be)) {
-        bv = ov;
-        be = oe;
-      }
-    }
+    const float mx = WaveMaxF(bv);
+    const int be = WaveMinI(bv == mx && bi < V ? bi * 64 + lane : 0x7fffffff);
     if ((be & 63) == lane) taken |= 1u << (be >> 6);
-    if (lane == k) mine = bv;
-    if (k == 0) sl0 = bv;
+    if (lane == k) mine = mx;
+    if (k == 0) top = mx;
     if (lane == 0) sel[(size_t)row * topk + k] = be;
   }
-  // Sum in rank order (lane 0 adds the ranks one by one).
-  const float ex = lane < topk ? __expf(mine - sl0) : 0.f;
+  const float ex = lane < topk ? __expf(mine - top) : 0.f;
+  float sum = 0.f;
   for (int k = 0; k < topk; ++k) sum += __shfl(ex, k, 64);
   if (lane < topk) wts[(size_t)row * (topk + 1) + lane] = ex / sum;
-  if (lane == 0) {
-    const float s = shared_logit ? shared_logit[row] : lg[E];
-    wts[(size_t)row * (topk + 1) + topk] = Sigmoid(s);
-  }
+  if (lane == 0) wts[(size_t)row * (topk + 1) + topk] = Sigmoid(shared_logit ? shared_logit[row] : lg[E]);
 }
 
 // ---- grouping --------------------------------------------------------------------------
@@ -132,47 +120,70 @@ __device__ int BlockExclusiveScan(int v, int* scratch, int* total) {
   return before;
 }
 
-// Whole grouping in one 1024-thread workgroup (up to kSmallRoutes routes): thread e
-// scans the routes in order and appends its expert's routes, so ranks are stable by
-// construction.  ref/prefill_ref.py:37-45.
+// Stable append of one route per thread (route index i in thread order; e < 0: none):
+// its position is cursor[e] + (routes of expert e in earlier waves) + (earlier lanes of
+// this wave with expert e).  Lanes of one expert are found by ballots over the id bits;
+// the waves take their cursor ranges in wave order, so positions follow route order.
+// Returns the position (or -1).  All threads of the block must call it.
+__device__ int StableAppend(int e, int* cursor) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const bool valid = e >= 0;
+  unsigned long long peers = __ballot(valid);
+#pragma unroll
+  for (int b = 0; b < 10; ++b) {
+    const bool bit = (e >> b) & 1;
+    const unsigned long long bb = __ballot(bit);
+    peers &= bit ? bb : ~bb;
+  }
+  const int rank = __popcll(peers & ((1ull << lane) - 1ull));
+  const int leader = valid ? __ffsll((long long)peers) - 1 : lane;
+  int base = 0;
+  for (int ww = 0; ww < nw; ++ww) {
+    if (w == ww && valid && rank == 0) base = atomicAdd(&cursor[e], __popcll(peers));
+    __syncthreads();
+  }
+  base = __shfl(base, leader, 64);
+  return valid ? base + rank : -1;
+}
+
+__device__ void WritePair(const GroupOut& o, int p, int i) {
+  o.pairs[p] = i;
+  o.row_ids[p] = i / o.topk;
+  if (o.inv) o.inv[i] = p;
+}
+
+// Whole grouping in one 1024-thread workgroup (up to kSmallRoutes routes).
+// ref/prefill_ref.py:37-45.
 __global__ void __launch_bounds__(1024) GroupSmallKernel(const int* __restrict__ sel, GroupOut o) {
-  __shared__ int s_sel[kSmallRoutes];
-  __shared__ int s_cnt[kMaxExperts];
+  __shared__ int s_cur[kMaxExperts];
   __shared__ int s_scan[128];
   const int n = o.M * o.topk;
-  for (int i = threadIdx.x; i < n; i += blockDim.x) s_sel[i] = sel[i];
+  for (int e = threadIdx.x; e < o.E; e += blockDim.x) s_cur[e] = 0;
   __syncthreads();
-  // Counts (one thread per expert, in route order).
-  for (int e = threadIdx.x; e < o.E; e += blockDim.x) {
-    int c = 0;
-    for (int i = 0; i < n; ++i) c += s_sel[i] == e;
-    s_cnt[e] = c;
-  }
+  for (int i = threadIdx.x; i < n; i += blockDim.x) atomicAdd(&s_cur[sel[i]], 1);  // counts only
   __syncthreads();
-  int total = 0, ctotal = 0;
-  // Offsets and entry bases: E <= 1024 experts, one per thread.
   const int e = threadIdx.x;
-  const int cnt = e < o.E ? s_cnt[e] : 0;
+  const int cnt = e < o.E ? s_cur[e] : 0;
+  int total = 0, ctotal = 0;
   const int off = BlockExclusiveScan(cnt, s_scan, &total);
   const int nch = o.entries ? (cnt + o.chunk - 1) / o.chunk : 0;
   const int chb = BlockExclusiveScan(nch, s_scan, &ctotal);
   if (e < o.E) {
     o.counts[e] = cnt;
     o.offsets[e] = off;
-    int p = off;
-    for (int i = 0; i < n && p < off + cnt; ++i)
-      if (s_sel[i] == e) {
-        o.pairs[p] = i;
-        o.row_ids[p] = i / o.topk;
-        if (o.inv) o.inv[i] = p;
-        ++p;
-      }
+    s_cur[e] = off;
     if (o.entries) WriteEntries(o, e, chb, cnt, off);
   }
   if (e == 0) o.offsets[o.E] = total;
   if (o.entries) {
     WriteSharedEntries(o, threadIdx.x, blockDim.x);
     if (threadIdx.x == 0) *o.n_entries = (o.M + o.chunk - 1) / o.chunk + ctotal;
+  }
+  __syncthreads();
+  for (int base = 0; base < n; base += blockDim.x) {
+    const int i = base + threadIdx.x;
+    const int p = StableAppend(i < n ? sel[i] : -1, s_cur);
+    if (p >= 0) WritePair(o, p, i);
   }
 }
 
@@ -225,23 +236,13 @@ __global__ void __launch_bounds__(1024) GroupScanKernel(int* __restrict__ tile_c
 
 __global__ void __launch_bounds__(1024) GroupScatterKernel(const int* __restrict__ sel, const int* __restrict__ tile_base,
                                                            int ntiles, GroupOut o) {
-  __shared__ int s_sel[kTile];
+  __shared__ int s_cur[kMaxExperts];
   const int n = o.M * o.topk;
-  const int t0 = blockIdx.x * kTile;
-  const int len = min(kTile, n - t0);
-  for (int i = threadIdx.x; i < len; i += blockDim.x) s_sel[i] = sel[t0 + i];
+  for (int e = threadIdx.x; e < o.E; e += blockDim.x) s_cur[e] = tile_base[(size_t)e * ntiles + blockIdx.x];
   __syncthreads();
-  for (int e = threadIdx.x; e < o.E; e += blockDim.x) {
-    int p = tile_base[(size_t)e * ntiles + blockIdx.x];
-    for (int i = 0; i < len; ++i)
-      if (s_sel[i] == e) {
-        const int r = t0 + i;
-        o.pairs[p] = r;
-        o.row_ids[p] = r / o.topk;
-        if (o.inv) o.inv[r] = p;
-        ++p;
-      }
-  }
+  const int i = blockIdx.x * kTile + threadIdx.x;
+  const int p = StableAppend(i < n ? sel[i] : -1, s_cur);
+  if (p >= 0) WritePair(o, p, i);
 }
 
 // ---- activation transforms of the experts ----------------------------------------------
@@ -253,16 +254,17 @@ struct ExpertTables {
 };
 
 // Gate and up input transforms of every compact row (each matrix has its own suh):
-// RoundH(x * suh) -> WHT128 -> * norm -> fp16 in MFMA row order.  engine/layers/moe_rows.h:102-125.
+// RoundH(x * suh) -> WHT128 -> * norm -> fp16 in MFMA row order, 16 lanes per block.
+// engine/layers/moe_rows.h:102-125.
 __global__ void __launch_bounds__(256) MoeInputKernel(const __half* __restrict__ x, const int* __restrict__ sel,
                                                       const int* __restrict__ pairs, ExpertTables tb, int M, int topk,
                                                       int E, int H, __half* __restrict__ xg, __half* __restrict__ xu) {
   const int nb = H / 128;
   const int P = M * topk + M;
-  const int item = (blockIdx.x * blockDim.x + threadIdx.x) >> 5;
+  const int item = (blockIdx.x * blockDim.x + threadIdx.x) >> 4;
   if (item >= P * nb * 2) return;
   const int mat = item & 1, blk = (item >> 1) % nb, p = (item >> 1) / nb;
-  const int j = threadIdx.x & 31;
+  const int j = threadIdx.x & 15;
   int row, e;
   if (p < M * topk) {
     const int route = pairs[p];
@@ -273,18 +275,14 @@ __global__ void __launch_bounds__(256) MoeInputKernel(const __half* __restrict__
     e = E;
   }
   const __half* suh = (mat ? tb.up : tb.gate)[e].suh;
-  const int c0 = blk * 128 + 4 * j;
-  const __half* xr = x + (size_t)row * H + c0;
-  float v[4];
+  const int c0 = blk * 128 + 8 * j;
+  float v[8], sv[8];
+  LoadH8(x + (size_t)row * H + c0, v);
+  LoadH8(suh + c0, sv);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) v[i] = RoundH(H2F(xr[i]) * H2F(suh[c0 + i]));
-  Wht128x4(v);
-  __half* d = (mat ? xu : xg) + (size_t)p * H + blk * 128;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int el = 4 * j + i;
-    d[(el & ~31) + PermPos32(el & 31)] = __float2half(v[i] * kHadNorm);
-  }
+  for (int i = 0; i < 8; ++i) v[i] = RoundH(v[i] * sv[i]);
+  Wht128x8(v);
+  StorePerm32x8((mat ? xu : xg) + (size_t)p * H + blk * 128, v, kHadNorm);
 }
 
 // Mid: gate and up output transforms (fp32), RoundH(RoundH(SiLU(g) * u) * suh_down),
@@ -295,62 +293,58 @@ __global__ void __launch_bounds__(256) MoeMidKernel(const float* __restrict__ yg
                                                     __half* __restrict__ xd) {
   const int nb = I / 128;
   const int P = M * topk + M;
-  const int item = (blockIdx.x * blockDim.x + threadIdx.x) >> 5;
+  const int item = (blockIdx.x * blockDim.x + threadIdx.x) >> 4;
   if (item >= P * nb) return;
   const int blk = item % nb, p = item / nb;
-  const int j = threadIdx.x & 31;
+  const int j = threadIdx.x & 15;
   const int e = p < M * topk ? sel[pairs[p]] : E;
-  const int c0 = blk * 128 + 4 * j;
-  const float4 g4 = *reinterpret_cast<const float4*>(yg + (size_t)p * I + c0);
-  const float4 u4 = *reinterpret_cast<const float4*>(yu + (size_t)p * I + c0);
-  float g[4] = {0.f + g4.x, 0.f + g4.y, 0.f + g4.z, 0.f + g4.w};
-  float u[4] = {0.f + u4.x, 0.f + u4.y, 0.f + u4.z, 0.f + u4.w};
-  Wht128x4(g);
-  Wht128x4(u);
-  const __half* svg = tb.gate[e].svh;
-  const __half* svu = tb.up[e].svh;
-  const __half* sud = tb.down[e].suh;
-  float v[4];
+  const int c0 = blk * 128 + 8 * j;
+  float g[8], u[8], svg[8], svu[8], sud[8];
+  LoadF8(yg + (size_t)p * I + c0, g);
+  LoadF8(yu + (size_t)p * I + c0, u);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float gv = g[i] * (kHadNorm * H2F(svg[c0 + i]));
-    const float uv = u[i] * (kHadNorm * H2F(svu[c0 + i]));
-    v[i] = RoundH(RoundH(SiLU(gv) * uv) * H2F(sud[c0 + i]));
+  for (int i = 0; i < 8; ++i) {
+    g[i] = 0.f + g[i];
+    u[i] = 0.f + u[i];
   }
-  Wht128x4(v);
-  __half* d = xd + (size_t)p * I + blk * 128;
+  Wht128x8(g);
+  Wht128x8(u);
+  LoadH8(tb.gate[e].svh + c0, svg);
+  LoadH8(tb.up[e].svh + c0, svu);
+  LoadH8(tb.down[e].suh + c0, sud);
+  float v[8];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int el = 4 * j + i;
-    d[(el & ~31) + PermPos32(el & 31)] = __float2half(v[i] * kHadNorm);
+  for (int i = 0; i < 8; ++i) {
+    const float gv = g[i] * (kHadNorm * svg[i]);
+    const float uv = u[i] * (kHadNorm * svu[i]);
+    v[i] = RoundH(RoundH(SiLU(gv) * uv) * sud[i]);
   }
+  Wht128x8(v);
+  StorePerm32x8(xd + (size_t)p * I + blk * 128, v, kHadNorm);
 }
 
-// Combine: per row and 128-block, slots 0..topk-1 in selection order then the shared
-// expert: y += w_k * (WHT(d_k) * (norm * svh_k)), fp32.  engine/layers/moe_rows.h:634-682.
-__global__ void __launch_bounds__(256) MoeCombineKernel(const float* __restrict__ yd, const int* __restrict__ sel,
-                                                        const float* __restrict__ wts, const int* __restrict__ inv,
-                                                        ExpertTables tb, int M, int topk, int E, int H,
+// Combine: per row, slots 0..topk-1 in selection order then the shared expert:
+// y += w_k * d_k, fp32, where d_k = WHT(y_h) * (norm * svh) came out of the down GEMM's
+// epilogue.  engine/layers/moe_rows.h:634-682.
+__global__ void __launch_bounds__(256) MoeCombineKernel(const float* __restrict__ pd, const float* __restrict__ wts,
+                                                        const int* __restrict__ inv, int M, int topk, int H,
                                                         float* __restrict__ y) {
-  const int nb = H / 128;
-  const int item = (blockIdx.x * blockDim.x + threadIdx.x) >> 5;
-  if (item >= M * nb) return;
-  const int blk = item % nb, r = item / nb;
-  const int j = threadIdx.x & 31;
-  const int c0 = blk * 128 + 4 * j;
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  const int nq = H / 4;
+  const int item = blockIdx.x * blockDim.x + threadIdx.x;
+  if (item >= M * nq) return;
+  const int r = item / nq, c0 = (item % nq) * 4;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 4
   for (int k = 0; k <= topk; ++k) {
     const int p = k < topk ? inv[r * topk + k] : M * topk + r;
-    const int e = k < topk ? sel[r * topk + k] : E;
+    const float4 d = *reinterpret_cast<const float4*>(pd + (size_t)p * H + c0);
     const float w = wts[(size_t)r * (topk + 1) + k];
-    const float4 d4 = *reinterpret_cast<const float4*>(yd + (size_t)p * H + c0);
-    float v[4] = {0.f + d4.x, 0.f + d4.y, 0.f + d4.z, 0.f + d4.w};
-    Wht128x4(v);
-    const __half* sv = tb.down[e].svh;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) acc[i] += w * (v[i] * (kHadNorm * H2F(sv[c0 + i])));
+    acc.x += w * d.x;
+    acc.y += w * d.y;
+    acc.z += w * d.z;
+    acc.w += w * d.w;
   }
-  *reinterpret_cast<float4*>(y + (size_t)r * H + c0) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+  *reinterpret_cast<float4*>(y + (size_t)r * H + c0) = acc;
 }
 
 }  // namespace cx
@@ -414,6 +408,15 @@ MoeSizes PlanMoe(const cx_moe_plan* pl, int M, int mode) {
   return s;
 }
 
+void LaunchRoute(const float* logits, int ld, int M, int E, int topk, const float* shared_logit, int* sel, float* wts,
+                 hipStream_t s) {
+  if (E <= 512)
+    hipLaunchKernelGGL(RouteKernel<8>, dim3((M + 3) / 4), dim3(256), 0, s, logits, ld, M, E, topk, shared_logit, sel, wts);
+  else
+    hipLaunchKernelGGL(RouteKernel<16>, dim3((M + 3) / 4), dim3(256), 0, s, logits, ld, M, E, topk, shared_logit, sel,
+                       wts);
+}
+
 int LaunchGroup(const int* sel, GroupOut& o, int* tile_counts, int ntiles, hipStream_t s) {
   const int n = o.M * o.topk;
   if (n <= kSmallRoutes) {
@@ -438,10 +441,12 @@ bool LaunchExpertGemm(const cx_moe_plan* pl, const MoeSizes& sz, bool gate_up, c
   g.S = 1;
   g.entries = ent;
   if (gate_up) {
-    g.plane[0] = GemmPlane{pl->tb.gate, xa, ya, in, out, 0};
-    g.plane[1] = GemmPlane{pl->tb.up, xb, yb, in, out, 0};
+    g.plane[0] = GemmPlane{pl->tb.gate, xa, ya, in, out, 0, 0};
+    g.plane[1] = GemmPlane{pl->tb.up, xb, yb, in, out, 0, 0};
   } else {
-    g.plane[0] = GemmPlane{pl->tb.down, xa, ya, in, out, 0};
+    // The down projection's output transform runs in the GEMM epilogue (a workgroup
+    // holds one whole 128-column block), so the combine is a plain weighted sum.
+    g.plane[0] = GemmPlane{pl->tb.down, xa, ya, in, out, 0, 1};
     g.plane[1] = g.plane[0];
   }
   const int ksw = gate_up ? 4 : 1;
@@ -484,8 +489,7 @@ int cx_moe_route(const float* logits, int32_t ld, int32_t M, int32_t E, int32_t 
   if (!logits || !sel || !wts) return CX_E_ARG;
   if (M <= 0 || E <= 0 || E > kMaxExperts || topk <= 0 || topk > kMaxTopK || topk > E || topk > 64) return CX_E_SHAPE;
   if (ld < E || (!shared_logit && ld < E + 1)) return CX_E_SHAPE;
-  hipLaunchKernelGGL(RouteKernel, dim3((M + 3) / 4), dim3(256), 0, (hipStream_t)stream, logits, ld, M, E, topk,
-                     shared_logit, sel, wts);
+  LaunchRoute(logits, ld, M, E, topk, shared_logit, sel, wts, (hipStream_t)stream);
   return LaunchStatus();
 }
 
@@ -616,15 +620,14 @@ int cx_moe_layer_forward(const cx_moe_plan* pl, const uint16_t* x, const float* 
     }
   };
   mark();
-  hipLaunchKernelGGL(RouteKernel, dim3((M + 3) / 4), dim3(256), 0, s, logits, ld, M, pl->E, pl->topk, shared_logit,
-                     sel, wts);
+  LaunchRoute(logits, ld, M, pl->E, pl->topk, shared_logit, sel, wts, s);
   mark();
   GroupOut o{counts, offsets, pairs, rows, inv, ent, nent, sz.chunk, M, pl->topk, pl->E};
   if ((rc = LaunchGroup(sel, o, tiles, sz.ntiles, s))) return rc;
   mark();
   {
     const long items = (long)sz.P * (pl->H / 128) * 2;
-    hipLaunchKernelGGL(MoeInputKernel, dim3((unsigned)((items * 32 + 255) / 256)), dim3(256), 0, s,
+    hipLaunchKernelGGL(MoeInputKernel, dim3((unsigned)((items * 16 + 255) / 256)), dim3(256), 0, s,
                        reinterpret_cast<const __half*>(x), sel, pairs, pl->tb, M, pl->topk, pl->E, pl->H, xg, xu);
   }
   mark();
@@ -632,16 +635,16 @@ int cx_moe_layer_forward(const cx_moe_plan* pl, const uint16_t* x, const float* 
   mark();
   {
     const long items = (long)sz.P * (pl->I / 128);
-    hipLaunchKernelGGL(MoeMidKernel, dim3((unsigned)((items * 32 + 255) / 256)), dim3(256), 0, s, yg, yu, sel, pairs,
+    hipLaunchKernelGGL(MoeMidKernel, dim3((unsigned)((items * 16 + 255) / 256)), dim3(256), 0, s, yg, yu, sel, pairs,
                        pl->tb, M, pl->topk, pl->E, pl->I, xd);
   }
   mark();
   if (!LaunchExpertGemm(pl, sz, false, xd, nullptr, yd, nullptr, ent, nent, s)) return CX_E_UNSUPPORTED;
   mark();
   {
-    const long items = (long)M * (pl->H / 128);
-    hipLaunchKernelGGL(MoeCombineKernel, dim3((unsigned)((items * 32 + 255) / 256)), dim3(256), 0, s, yd, sel, wts,
-                       inv, pl->tb, M, pl->topk, pl->E, pl->H, y);
+    const long items = (long)M * (pl->H / 4);
+    hipLaunchKernelGGL(MoeCombineKernel, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, s, yd, wts, inv, M,
+                       pl->topk, pl->H, y);
   }
   mark();
   return LaunchStatus();
