@@ -68,8 +68,12 @@ void FillLinearTables(int4* ent, MatPtr* mat, const LinearPlan& p, int M, const 
 // Launches Exl3GemmKernel for a runtime (rate, codebook, rows per wave, waves per
 // column pair).  Returns false for an unsupported combination.
 bool LaunchGemm(int k2, int cb, int nrb, int ksw, int u, dim3 grid, const GemmArgs& g, hipStream_t s);
+// The decode-once prefill GEMM (Exl3GemmPrefillKernel): grid (O / 128, entries, planes).
+bool LaunchGemmPrefill(int k2, int cb, int nrb, dim3 grid, const GemmArgs& g, hipStream_t s);
 // Per-rate launchers (one translation unit per rate, gemm_inst.hip).
-#define CX_DECLARE_RATE(K2) bool LaunchGemmRate##K2(int cb, int nrb, int ksw, dim3 grid, const GemmArgs& g, hipStream_t s);
+#define CX_DECLARE_RATE(K2)                                                                          \
+  bool LaunchGemmRate##K2(int cb, int nrb, int ksw, dim3 grid, const GemmArgs& g, hipStream_t s); \
+  bool LaunchGemmPrefillRate##K2(int cb, int nrb, dim3 grid, const GemmArgs& g, hipStream_t s);
 CX_DECLARE_RATE(2)
 CX_DECLARE_RATE(3)
 CX_DECLARE_RATE(4)

@@ -365,10 +365,20 @@ namespace cx {
 
 struct MoeSizes {
   int M, P, n, nsh, chunk, nrb, max_entries, ntiles;
-  bool small;
+  bool small, prefill;
   size_t off_sel, off_wts, off_counts, off_offsets, off_pairs, off_rows, off_inv, off_ent, off_nent, off_tiles;
   size_t off_xg, off_xu, off_yg, off_yu, off_xd, off_yd, total;
 };
+
+// Row blocks per wave of the prefill GEMM (4 waves x 16 NRB rows share each decoded tile).
+int PrefillRowBlocks() {
+  static const int nrb = [] {
+    const char* e = std::getenv("CX_PREFILL_NRB");
+    const int v = e ? std::atoi(e) : 2;
+    return v == 4 ? 4 : 2;
+  }();
+  return nrb;
+}
 
 MoeSizes PlanMoe(const cx_moe_plan* pl, int M, int mode) {
   MoeSizes s{};
@@ -376,8 +386,10 @@ MoeSizes PlanMoe(const cx_moe_plan* pl, int M, int mode) {
   s.n = M * pl->topk;
   s.P = s.n + M;
   const bool decode = mode == CX_MOE_DECODE || (mode == CX_MOE_AUTO && M <= 64);
-  s.nrb = decode ? 1 : 4;
-  s.chunk = 16 * s.nrb;
+  s.prefill = !decode;
+  s.nrb = decode ? 1 : PrefillRowBlocks();
+  // Decode: one 16-row block per entry; prefill: up to 4 x 16 NRB rows share each decoded tile.
+  s.chunk = decode ? 16 : 64 * s.nrb;
   s.nsh = (M + s.chunk - 1) / s.chunk;
   s.max_entries = s.nsh + std::min(pl->E, s.n) + s.n / s.chunk;
   s.small = s.n <= kSmallRoutes;
@@ -453,19 +465,23 @@ bool LaunchExpertGemm(const cx_moe_plan* pl, const MoeSizes& sz, bool gate_up, c
   const int planes = gate_up ? 2 : 1;
   const int k2r = gate_up ? pl->k2_gu : pl->k2_d, cbr = gate_up ? pl->cb_gu : pl->cb_d;
   const int k2s = gate_up ? pl->k2_sgu : pl->k2_sd, cbs = gate_up ? pl->cb_sgu : pl->cb_sd;
-  const int cpg = g.ncp / (4 / ksw);
+  const int cpg = sz.prefill ? g.ncp / 4 : g.ncp / (4 / ksw);
+  auto launch = [&](int k2, int cb, int ny) {
+    const dim3 grid(cpg, ny, planes);
+    return sz.prefill ? LaunchGemmPrefill(k2, cb, sz.nrb, grid, g, s) : LaunchGemm(k2, cb, sz.nrb, ksw, 4, grid, g, s);
+  };
   if (k2r == k2s && cbr == cbs) {
     g.n_entries = nent;
     g.entry_base = 0;
-    return LaunchGemm(k2r, cbr, sz.nrb, ksw, 4, dim3(cpg, sz.max_entries, planes), g, s);
+    return launch(k2r, cbr, sz.max_entries);
   }
   g.n_entries = nullptr;
   g.n_entries_host = sz.nsh;
   g.entry_base = 0;
-  if (!LaunchGemm(k2s, cbs, sz.nrb, ksw, 4, dim3(cpg, sz.nsh, planes), g, s)) return false;
+  if (!launch(k2s, cbs, sz.nsh)) return false;
   g.n_entries = nent;
   g.entry_base = sz.nsh;
-  return LaunchGemm(k2r, cbr, sz.nrb, ksw, 4, dim3(cpg, sz.max_entries - sz.nsh, planes), g, s);
+  return launch(k2r, cbr, sz.max_entries - sz.nsh);
 }
 
 int CheckExpertShapes(const cx_moe_expert& ex, int H, int I) {
