@@ -182,6 +182,23 @@ bool LaunchGemm(int k2, int cb, int nrb, int ksw, int u, dim3 grid, const GemmAr
   }
 }
 
+bool LaunchGemmPrefill2(int k2, int cb, int nrbt, int cpwv, dim3 grid, const GemmArgs& g, hipStream_t s) {
+  switch (k2) {
+    case 2: return LaunchGemmPrefill2Rate2(cb, nrbt, cpwv, grid, g, s);
+    case 3: return LaunchGemmPrefill2Rate3(cb, nrbt, cpwv, grid, g, s);
+    case 4: return LaunchGemmPrefill2Rate4(cb, nrbt, cpwv, grid, g, s);
+    case 5: return LaunchGemmPrefill2Rate5(cb, nrbt, cpwv, grid, g, s);
+    case 6: return LaunchGemmPrefill2Rate6(cb, nrbt, cpwv, grid, g, s);
+    case 7: return LaunchGemmPrefill2Rate7(cb, nrbt, cpwv, grid, g, s);
+    case 8: return LaunchGemmPrefill2Rate8(cb, nrbt, cpwv, grid, g, s);
+    case 10: return LaunchGemmPrefill2Rate10(cb, nrbt, cpwv, grid, g, s);
+    case 12: return LaunchGemmPrefill2Rate12(cb, nrbt, cpwv, grid, g, s);
+    case 14: return LaunchGemmPrefill2Rate14(cb, nrbt, cpwv, grid, g, s);
+    case 16: return LaunchGemmPrefill2Rate16(cb, nrbt, cpwv, grid, g, s);
+    default: return false;
+  }
+}
+
 bool LaunchGemmPrefill(int k2, int cb, int nrb, dim3 grid, const GemmArgs& g, hipStream_t s) {
   switch (k2) {
     case 2: return LaunchGemmPrefillRate2(cb, nrb, grid, g, s);

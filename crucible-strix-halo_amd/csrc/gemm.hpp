@@ -428,3 +428,231 @@ __global__ void __launch_bounds__(512) Exl3GemmPrefillKernel(GemmArgs g) {
 }
 
 }  // namespace cx
+
+namespace cx {
+
+// Prefill variant 2 (register-blocked): a workgroup = 4 waves owns 4 CPWV column pairs
+// (128 CPWV columns) x up to 16 NRBT rows of one expert, full K.  Each wave decodes its
+// own CPWV column pairs (B fragments stay in registers, every tile decoded once per
+// workgroup) and multiplies them with all the workgroup's row blocks; the activation
+// tile of a step (16 NRBT rows x 32 inputs) is loaded once into LDS and shared by the 4
+// waves.  One barrier per step double-buffers the activation tile.
+template <int K2, int CB, int NRBT, int CPWV>
+__global__ void __launch_bounds__(256) Exl3GemmPrefill2Kernel(GemmArgs g) {
+  constexpr int T = TileDwords(K2);
+  constexpr int SD = 4 * T;
+  constexpr int DPL = (SD + 63) / 64;
+  constexpr int ND = WindowDwords(K2);
+  constexpr int R = 16 * NRBT;          // rows per workgroup
+  constexpr int XS = 40;                // halves per staged row (32 + 8 pad: conflict-free 16 B reads)
+  constexpr int XL = (R * 4 + 255) / 256;  // 16-byte activation loads per thread per step
+  constexpr int XBYTES = 2 * R * XS * 2, EBYTES = 64 * 132 * 4;
+  __shared__ uint32_t stage[4][CPWV][StageDwords<DPL>()];
+  // Activation tiles during the main loop; the epilogue's row staging afterwards.
+  __shared__ __align__(16) char smem[XBYTES > EBYTES ? XBYTES : EBYTES];
+  __half(*xs)[R][XS] = reinterpret_cast<__half(*)[R][XS]>(smem);
+  const int n_entries = g.n_entries ? *g.n_entries : g.n_entries_host;
+  const int ei = (int)blockIdx.y + g.entry_base;
+  if (ei >= n_entries) return;
+  const int4 ent = g.entries[ei];
+  const GemmPlane& pl = g.plane[blockIdx.z];
+  const int cpg = blockIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int steps = g.A / 2;
+  const int row0 = ent.y, nrows = ent.z;
+  const int nrb = (nrows + 15) / 16;
+  const MatPtr m = pl.mats[ent.x];
+  const LaneRun<K2> lr(lane);
+
+  __amdgpu_buffer_rsrc_t rw[CPWV];
+#pragma unroll
+  for (int c = 0; c < CPWV; ++c) {
+    const int cp = (cpg * 4 + wave) * CPWV + c;
+    rw[c] = MakeRsrc(m.tiles + (size_t)cp * g.A * 2 * T, (uint32_t)steps * SD * 4);
+  }
+  uint32_t woff[2][ND];
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int i = 0; i < ND; ++i) woff[j][i] = (uint32_t)StagePad((2 * j + lr.tile) * T + (lr.d0 + i) % T);
+  const uint32_t loff = (uint32_t)lane * DPL * 4;
+
+  // Activation tile loads: thread t moves rows t / 4 + 64 i, quarter t % 4 (16 bytes).
+  const __amdgpu_buffer_rsrc_t rx = MakeRsrc(pl.x + (size_t)row0 * pl.ldx, (uint32_t)nrows * pl.ldx * 2);
+  uint32_t xoff[XL];
+#pragma unroll
+  for (int i = 0; i < XL; ++i) {
+    const int row = (int)threadIdx.x / 4 + 64 * i;
+    xoff[i] = (uint32_t)((row * pl.ldx + 8 * (threadIdx.x & 3)) * 2);
+  }
+  auto load_x = [&](u32x4_t (&xv)[XL], int s) {
+#pragma unroll
+    for (int i = 0; i < XL; ++i) xv[i] = BufLoad128(rx, xoff[i], (uint32_t)s * 64);
+  };
+  auto store_x = [&](const u32x4_t (&xv)[XL], int buf) {
+#pragma unroll
+    for (int i = 0; i < XL; ++i) {
+      const int row = (int)threadIdx.x / 4 + 64 * i;
+      if (row < R) *reinterpret_cast<u32x4_t*>(&xs[buf][row][8 * (threadIdx.x & 3)]) = xv[i];
+    }
+  };
+
+  float4_t acc[NRBT][CPWV][2];
+#pragma unroll
+  for (int i = 0; i < NRBT; ++i)
+#pragma unroll
+    for (int c = 0; c < CPWV; ++c) acc[i][c][0] = acc[i][c][1] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+  constexpr int PFW = 6;  // weight steps in flight
+  constexpr int PFX = 3;  // activation steps in flight
+  Dwords<DPL> wq[PFW][CPWV];
+  u32x4_t xq[PFX][XL];
+#pragma unroll
+  for (int k = 0; k < PFW; ++k)
+    if (k < steps)
+#pragma unroll
+      for (int c = 0; c < CPWV; ++c) wq[k][c] = BufLoadN<DPL>(rw[c], loff, (uint32_t)k * SD * 4);
+#pragma unroll
+  for (int k = 0; k < PFX; ++k)
+    if (k < steps) load_x(xq[k], k);
+  store_x(xq[0], 0);
+  if (PFX < steps) load_x(xq[0], PFX);
+  __syncthreads();
+
+  uint32_t* slot[CPWV];
+#pragma unroll
+  for (int c = 0; c < CPWV; ++c) slot[c] = stage[wave][c];
+
+  // The main loop is instantiated per count of live row blocks NA, so the accumulators
+  // stay in fixed registers (a runtime guard per MFMA makes the compiler copy them).
+  auto main_loop = [&](auto nac) {
+    constexpr int NA = decltype(nac)::value;
+    // Steps are unrolled by lcm(PFW, PFX) = 6 so every queue slot is a fixed register set.
+    constexpr int UN = 6;
+    for (int s0 = 0; s0 < steps; s0 += UN) {
+#pragma unroll
+      for (int u = 0; u < UN; ++u) {
+        const int s = s0 + u;
+        if (s >= steps) break;
+        const int qw = u % PFW, qx = (u + 1) % PFX;
+        // Next step's activations into the other tile buffer; refill that queue slot.
+        if (s + 1 < steps) {
+          store_x(xq[qx], (s + 1) & 1);
+          if (s + 1 + PFX < steps) load_x(xq[qx], s + 1 + PFX);
+        }
+        // Decode this wave's column pairs for step s.
+        half8_t b[CPWV][2];
+#pragma unroll
+        for (int c = 0; c < CPWV; ++c) {
+          StageWrite<DPL>(slot[c], lane, wq[qw][c].v);
+          __builtin_amdgcn_wave_barrier();
+          uint32_t v[2][3];
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+#pragma unroll
+            for (int i = 0; i < ND; ++i) v[j][i] = slot[c][woff[j][i]];
+            if constexpr (ND == 2) v[j][2] = 0u;
+          }
+          __builtin_amdgcn_wave_barrier();
+          if (s + PFW < steps) wq[qw][c] = BufLoadN<DPL>(rw[c], loff, (uint32_t)(s + PFW) * SD * 4);
+          half4_t lo0, hi0, lo1, hi1;
+          DecodeRun<K2, CB>(v[0][0], v[0][1], v[0][2], lr.shift, lo0, hi0);
+          DecodeRun<K2, CB>(v[1][0], v[1][1], v[1][2], lr.shift, lo1, hi1);
+          b[c][0] = half8_t{lo0[0], lo0[1], lo0[2], lo0[3], lo1[0], lo1[1], lo1[2], lo1[3]};
+          b[c][1] = half8_t{hi0[0], hi0[1], hi0[2], hi0[3], hi1[0], hi1[1], hi1[2], hi1[3]};
+        }
+        const int buf = s & 1;
+#pragma unroll
+        for (int i = 0; i < NRBT; ++i) {
+          if (i < NA) {
+            const half8_t av = *reinterpret_cast<const half8_t*>(&xs[buf][i * 16 + (lane & 15)][8 * (lane >> 4)]);
+#pragma unroll
+            for (int c = 0; c < CPWV; ++c) {
+              acc[i][c][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b[c][0], acc[i][c][0], 0, 0, 0);
+              acc[i][c][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b[c][1], acc[i][c][1], 0, 0, 0);
+            }
+          }
+        }
+        __syncthreads();
+      }
+    }
+  };
+  using std::integral_constant;
+  if (nrb <= 1) main_loop(integral_constant<int, 1>{});
+  else if (nrb == 2) main_loop(integral_constant<int, 2>{});
+  else if (nrb == 3) main_loop(integral_constant<int, 3>{});
+  else if (nrb == 4 || NRBT == 4) main_loop(integral_constant<int, 4>{});
+  else if constexpr (NRBT == 8) {
+    if (nrb == 5) main_loop(integral_constant<int, 5>{});
+    else if (nrb == 6) main_loop(integral_constant<int, 6>{});
+    else if (nrb == 7) main_loop(integral_constant<int, 7>{});
+    else main_loop(integral_constant<int, 8>{});
+  }
+
+  if (pl.epi == 1) {
+    // Output transform per 128-column block: stage y_h rows in LDS (reusing the
+    // activation tile area), WHT128 * norm * svh per row.
+    float(*eb)[132] = reinterpret_cast<float(*)[132]>(smem);
+    const int j = threadIdx.x & 15;
+#pragma unroll
+    for (int blk = 0; blk < CPWV; ++blk) {
+      // Column block blk of this workgroup holds column pairs 4 blk .. 4 blk + 3 of the
+      // workgroup = waves (4 blk + q) / CPWV, their pair (4 blk + q) % CPWV.
+      const int c0 = (cpg * CPWV + blk) * 128 + 8 * j;
+      float sv[8];
+      LoadH8(m.svh + c0, sv);
+      for (int r0 = 0; r0 < nrows; r0 += 64) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int wpair = 4 * blk + q;  // column pair index within the workgroup
+          if (wave == wpair / CPWV) {
+            const int c = wpair % CPWV;
+            const int cl = q * 32 + ((lane & 15) >> 3) * 16 + (lane & 7);
+#pragma unroll
+            for (int i = 0; i < NRBT; ++i) {
+              if (i * 16 < r0 || i * 16 >= r0 + 64) continue;
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const int r = i * 16 - r0 + 4 * (lane >> 4) + e;
+                eb[r][cl] = acc[i][c][0][e];
+                eb[r][cl + 8] = acc[i][c][1][e];
+              }
+            }
+          }
+        }
+        __syncthreads();
+        for (int rr = threadIdx.x >> 4; rr < 64 && r0 + rr < nrows; rr += 16) {
+          float v[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[e] = 0.f + eb[rr][8 * j + e];
+          Wht128x8(v);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[e] *= kHadNorm * sv[e];
+          StoreF8(pl.y + (size_t)(row0 + r0 + rr) * pl.ldy + c0, v);
+        }
+        __syncthreads();
+      }
+    }
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < NRBT; ++i) {
+    if (i >= nrb) break;
+#pragma unroll
+    for (int c = 0; c < CPWV; ++c) {
+      const int cp = (cpg * 4 + wave) * CPWV + c;
+      const int col = (2 * cp + ((lane & 15) >> 3)) * 16 + (lane & 7);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int r = i * 16 + 4 * (lane >> 4) + e;
+        if (r < nrows) {
+          float* yr = pl.y + (size_t)(row0 + r) * pl.ldy;
+          yr[col] = acc[i][c][0][e];
+          yr[col + 8] = acc[i][c][1][e];
+        }
+      }
+    }
+  }
+}
+
+}  // namespace cx

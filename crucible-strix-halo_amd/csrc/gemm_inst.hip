@@ -62,4 +62,26 @@ bool CX_CAT(LaunchGemmPrefillRate, CX_RATE)(int cb, int nrb, dim3 grid, const Ge
   return false;
 }
 
+bool CX_CAT(LaunchGemmPrefill2Rate, CX_RATE)(int cb, int nrbt, int cpwv, dim3 grid, const GemmArgs& g, hipStream_t s) {
+  constexpr int K2 = CX_RATE;
+  auto go = [&](auto cbc, auto nc, auto cc) {
+    constexpr int CB = decltype(cbc)::value, NRBT = decltype(nc)::value, CPWV = decltype(cc)::value;
+    hipLaunchKernelGGL((Exl3GemmPrefill2Kernel<K2, CB, NRBT, CPWV>), grid, dim3(256), 0, s, g);
+    return true;
+  };
+  auto shape = [&](auto cbc) {
+    if (nrbt == 4 && cpwv == 1) return go(cbc, IC<4>{}, IC<1>{});
+    if (nrbt == 8 && cpwv == 1) return go(cbc, IC<8>{}, IC<1>{});
+    if (nrbt == 4 && cpwv == 2) return go(cbc, IC<4>{}, IC<2>{});
+    if (nrbt == 8 && cpwv == 2) return go(cbc, IC<8>{}, IC<2>{});
+    return false;
+  };
+  if (cb == kCbMul1) return shape(IC<kCbMul1>{});
+  if constexpr (K2 % 2 == 0) {
+    if (cb == kCbMcg) return shape(IC<kCbMcg>{});
+    if (cb == kCb3Inst) return shape(IC<kCb3Inst>{});
+  }
+  return false;
+}
+
 }  // namespace cx
