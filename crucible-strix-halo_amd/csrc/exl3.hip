@@ -182,39 +182,23 @@ bool LaunchGemm(int k2, int cb, int nrb, int ksw, int u, dim3 grid, const GemmAr
   }
 }
 
-bool LaunchGemmPrefill2(int k2, int cb, int nrbt, int cpwv, dim3 grid, const GemmArgs& g, hipStream_t s) {
+bool LaunchGemmPrefill(int k2, int cb, int nrbt, int cpwv, dim3 grid, const GemmArgs& g, hipStream_t s) {
   switch (k2) {
-    case 2: return LaunchGemmPrefill2Rate2(cb, nrbt, cpwv, grid, g, s);
-    case 3: return LaunchGemmPrefill2Rate3(cb, nrbt, cpwv, grid, g, s);
-    case 4: return LaunchGemmPrefill2Rate4(cb, nrbt, cpwv, grid, g, s);
-    case 5: return LaunchGemmPrefill2Rate5(cb, nrbt, cpwv, grid, g, s);
-    case 6: return LaunchGemmPrefill2Rate6(cb, nrbt, cpwv, grid, g, s);
-    case 7: return LaunchGemmPrefill2Rate7(cb, nrbt, cpwv, grid, g, s);
-    case 8: return LaunchGemmPrefill2Rate8(cb, nrbt, cpwv, grid, g, s);
-    case 10: return LaunchGemmPrefill2Rate10(cb, nrbt, cpwv, grid, g, s);
-    case 12: return LaunchGemmPrefill2Rate12(cb, nrbt, cpwv, grid, g, s);
-    case 14: return LaunchGemmPrefill2Rate14(cb, nrbt, cpwv, grid, g, s);
-    case 16: return LaunchGemmPrefill2Rate16(cb, nrbt, cpwv, grid, g, s);
+    case 2: return LaunchGemmPrefillRate2(cb, nrbt, cpwv, grid, g, s);
+    case 3: return LaunchGemmPrefillRate3(cb, nrbt, cpwv, grid, g, s);
+    case 4: return LaunchGemmPrefillRate4(cb, nrbt, cpwv, grid, g, s);
+    case 5: return LaunchGemmPrefillRate5(cb, nrbt, cpwv, grid, g, s);
+    case 6: return LaunchGemmPrefillRate6(cb, nrbt, cpwv, grid, g, s);
+    case 7: return LaunchGemmPrefillRate7(cb, nrbt, cpwv, grid, g, s);
+    case 8: return LaunchGemmPrefillRate8(cb, nrbt, cpwv, grid, g, s);
+    case 10: return LaunchGemmPrefillRate10(cb, nrbt, cpwv, grid, g, s);
+    case 12: return LaunchGemmPrefillRate12(cb, nrbt, cpwv, grid, g, s);
+    case 14: return LaunchGemmPrefillRate14(cb, nrbt, cpwv, grid, g, s);
+    case 16: return LaunchGemmPrefillRate16(cb, nrbt, cpwv, grid, g, s);
     default: return false;
   }
 }
 
-bool LaunchGemmPrefill(int k2, int cb, int nrb, dim3 grid, const GemmArgs& g, hipStream_t s) {
-  switch (k2) {
-    case 2: return LaunchGemmPrefillRate2(cb, nrb, grid, g, s);
-    case 3: return LaunchGemmPrefillRate3(cb, nrb, grid, g, s);
-    case 4: return LaunchGemmPrefillRate4(cb, nrb, grid, g, s);
-    case 5: return LaunchGemmPrefillRate5(cb, nrb, grid, g, s);
-    case 6: return LaunchGemmPrefillRate6(cb, nrb, grid, g, s);
-    case 7: return LaunchGemmPrefillRate7(cb, nrb, grid, g, s);
-    case 8: return LaunchGemmPrefillRate8(cb, nrb, grid, g, s);
-    case 10: return LaunchGemmPrefillRate10(cb, nrb, grid, g, s);
-    case 12: return LaunchGemmPrefillRate12(cb, nrb, grid, g, s);
-    case 14: return LaunchGemmPrefillRate14(cb, nrb, grid, g, s);
-    case 16: return LaunchGemmPrefillRate16(cb, nrb, grid, g, s);
-    default: return false;
-  }
-}
 
 size_t LinearWorkspace(const LinearPlan& p, int I, int O, int M) {
   const size_t xp = AlignUp((size_t)M * I * 2, 256);

@@ -249,196 +249,27 @@ __global__ void __launch_bounds__(256) Exl3GemmKernel(GemmArgs g) {
 
 namespace cx {
 
-// Prefill variant (producer / consumer): one workgroup = 8 waves, 128 output columns
-// (4 column pairs) x up to 64 NRB rows of one expert, full K.  Waves 0-3 produce: wave p
-// decodes column pair 4 cpg + p, one step (two k-tiles) per iteration, and writes each
-// lane's two MFMA B fragments to an LDS ring.  Waves 4-7 consume: wave c applies all four
-// column pairs' fragments of the previous step to its row blocks (c, c + 4, ...).  Every
-// weight tile is decoded once per workgroup, and on each SIMD a producer's decode
-// (VALU) overlaps a consumer's MFMAs.  One barrier per step hands the ring over.
-template <int K2, int CB, int NRB>
-__global__ void __launch_bounds__(512) Exl3GemmPrefillKernel(GemmArgs g) {
-  constexpr int T = TileDwords(K2);
-  constexpr int SD = 4 * T;
-  constexpr int DPL = (SD + 63) / 64;
-  constexpr int ND = WindowDwords(K2);
-  __shared__ uint32_t stage[4][StageDwords<DPL>()];
-  __shared__ half8_t frag[2][4][2][64];  // [ring slot][column pair][MFMA][lane]
-  const int n_entries = g.n_entries ? *g.n_entries : g.n_entries_host;
-  const int ei = (int)blockIdx.y + g.entry_base;
-  if (ei >= n_entries) return;
-  const int4 ent = g.entries[ei];
-  const GemmPlane& pl = g.plane[blockIdx.z];
-  const int cpg = blockIdx.x;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  const bool producer = wave < 4;
-  const int role = wave & 3;
-  const int steps = g.A / 2;
-  const int row0 = ent.y, nrows = ent.z;
-  const MatPtr m = pl.mats[ent.x];
-  const int nrb_all = (nrows + 15) / 16;
-  const int my_rb = nrb_all > role ? (nrb_all - role + 3) / 4 : 0;
-
-  float4_t acc[NRB][4][2];
-#pragma unroll
-  for (int i = 0; i < NRB; ++i)
-#pragma unroll
-    for (int c = 0; c < 4; ++c) acc[i][c][0] = acc[i][c][1] = float4_t{0.f, 0.f, 0.f, 0.f};
-
-  constexpr int PF = 4;  // steps in flight ahead (weights for producers, activations for consumers)
-  if (producer) {
-    const int cp = cpg * 4 + role;
-    const __amdgpu_buffer_rsrc_t rw = MakeRsrc(m.tiles + (size_t)cp * g.A * 2 * T, (uint32_t)steps * SD * 4);
-    const LaneRun<K2> lr(lane);
-    uint32_t woff[2][ND];
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int i = 0; i < ND; ++i) woff[j][i] = (uint32_t)StagePad((2 * j + lr.tile) * T + (lr.d0 + i) % T);
-    const uint32_t loff = (uint32_t)lane * DPL * 4;
-    uint32_t* slot = stage[role];
-    Dwords<DPL> wq[PF];
-#pragma unroll
-    for (int k = 0; k < PF; ++k)
-      if (k < steps) wq[k] = BufLoadN<DPL>(rw, loff, (uint32_t)k * SD * 4);
-    for (int s0 = 0; s0 <= steps; s0 += PF) {
-#pragma unroll
-      for (int u = 0; u < PF; ++u) {
-        const int it = s0 + u;
-        if (it > steps) break;
-        if (it < steps) {
-          StageWrite<DPL>(slot, lane, wq[u].v);
-          __builtin_amdgcn_wave_barrier();
-          uint32_t v[2][3];
-#pragma unroll
-          for (int j = 0; j < 2; ++j) {
-#pragma unroll
-            for (int i = 0; i < ND; ++i) v[j][i] = slot[woff[j][i]];
-            if constexpr (ND == 2) v[j][2] = 0u;
-          }
-          __builtin_amdgcn_wave_barrier();
-          if (it + PF < steps) wq[u] = BufLoadN<DPL>(rw, loff, (uint32_t)(it + PF) * SD * 4);
-          half4_t lo0, hi0, lo1, hi1;
-          DecodeRun<K2, CB>(v[0][0], v[0][1], v[0][2], lr.shift, lo0, hi0);
-          DecodeRun<K2, CB>(v[1][0], v[1][1], v[1][2], lr.shift, lo1, hi1);
-          frag[it & 1][role][0][lane] = half8_t{lo0[0], lo0[1], lo0[2], lo0[3], lo1[0], lo1[1], lo1[2], lo1[3]};
-          frag[it & 1][role][1][lane] = half8_t{hi0[0], hi0[1], hi0[2], hi0[3], hi1[0], hi1[1], hi1[2], hi1[3]};
-        }
-        __syncthreads();
-      }
-    }
-  } else {
-    const __amdgpu_buffer_rsrc_t rx = MakeRsrc(pl.x + (size_t)row0 * pl.ldx, (uint32_t)nrows * pl.ldx * 2);
-    uint32_t xoff[NRB];
-#pragma unroll
-    for (int i = 0; i < NRB; ++i)
-      xoff[i] = (uint32_t)((((role + 4 * i) * 16 + (lane & 15)) * pl.ldx + 8 * (lane >> 4)) * 2);
-    u32x4_t xq[PF][NRB];
-    auto load_x = [&](u32x4_t (&x)[NRB], int st) {
-#pragma unroll
-      for (int i = 0; i < NRB; ++i)
-        x[i] = i < my_rb ? BufLoad128(rx, xoff[i], (uint32_t)st * 64) : u32x4_t{0u, 0u, 0u, 0u};
-    };
-#pragma unroll
-    for (int k = 0; k < PF; ++k)
-      if (k < steps) load_x(xq[k], k);
-    // Iteration it multiplies step it - 1 (slot u - 1 of the queue).
-    for (int s0 = 0; s0 <= steps; s0 += PF) {
-#pragma unroll
-      for (int u = 0; u < PF; ++u) {
-        const int it = s0 + u;
-        if (it > steps) break;
-        if (it >= 1) {
-          const int s = it - 1, q = (u + PF - 1) % PF, b = s & 1;
-#pragma unroll
-          for (int c = 0; c < 4; ++c) {
-            const half8_t b0 = frag[b][c][0][lane], b1 = frag[b][c][1][lane];
-#pragma unroll
-            for (int i = 0; i < NRB; ++i) {
-              if (i < my_rb) {
-                const half8_t av = __builtin_bit_cast(half8_t, xq[q][i]);
-                acc[i][c][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b0, acc[i][c][0], 0, 0, 0);
-                acc[i][c][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b1, acc[i][c][1], 0, 0, 0);
-              }
-            }
-          }
-          if (s + PF < steps) load_x(xq[q], s + PF);
-        }
-        __syncthreads();
-      }
-    }
-  }
-
-  if (pl.epi == 1) {
-    // Output transform per 64-row slab: consumers stage y_h in LDS, then all 512 threads
-    // apply WHT128 * norm * svh per row (16 lanes per row).
-    __shared__ float ebuf[64][132];
-    const int j = threadIdx.x & 15, c0 = cpg * 128 + 8 * j;
-    float sv[8];
-    LoadH8(m.svh + c0, sv);
-#pragma unroll
-    for (int i = 0; i < NRB; ++i) {
-      if (i * 64 >= nrows) break;  // uniform
-      if (!producer) {
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const int cl = c * 32 + ((lane & 15) >> 3) * 16 + (lane & 7);
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const int r = role * 16 + 4 * (lane >> 4) + q;
-            ebuf[r][cl] = acc[i][c][0][q];
-            ebuf[r][cl + 8] = acc[i][c][1][q];
-          }
-        }
-      }
-      __syncthreads();
-      for (int rr = threadIdx.x >> 4; rr < 64; rr += 32) {
-        const int r = 16 * ((rr >> 4) + 4 * i) + (rr & 15);
-        if (r >= nrows) continue;  // whole 16-lane rows
-        float v[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = 0.f + ebuf[rr][8 * j + e];
-        Wht128x8(v);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] *= kHadNorm * sv[e];
-        StoreF8(pl.y + (size_t)(row0 + r) * pl.ldy + c0, v);
-      }
-      __syncthreads();
-    }
-    return;
-  }
-  if (producer) return;
-#pragma unroll
-  for (int i = 0; i < NRB; ++i) {
-    if (i >= my_rb) break;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int col = (2 * (cpg * 4 + c) + ((lane & 15) >> 3)) * 16 + (lane & 7);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int r = (role + 4 * i) * 16 + 4 * (lane >> 4) + q;
-        if (r < nrows) {
-          float* yr = pl.y + (size_t)(row0 + r) * pl.ldy;
-          yr[col] = acc[i][c][0][q];
-          yr[col + 8] = acc[i][c][1][q];
-        }
-      }
-    }
-  }
-}
-
-}  // namespace cx
-
-namespace cx {
-
-// Prefill variant 2 (register-blocked): a workgroup = 4 waves owns 4 CPWV column pairs
+// Prefill GEMM (register-blocked): a workgroup = 4 waves owns 4 CPWV column pairs
 // (128 CPWV columns) x up to 16 NRBT rows of one expert, full K.  Each wave decodes its
 // own CPWV column pairs (B fragments stay in registers, every tile decoded once per
 // workgroup) and multiplies them with all the workgroup's row blocks; the activation
 // tile of a step (16 NRBT rows x 32 inputs) is loaded once into LDS and shared by the 4
 // waves.  One barrier per step double-buffers the activation tile.
+// Workgroups go to the 8 XCDs round-robin by linear id.  This remap puts all gridDim.x *
+// gridDim.z workgroups of row entry y on XCD y % 8, consecutively, so an entry's activation
+// rows are fetched into one L2 and reused there.  gridDim.y must be a multiple of 8.
+struct GridPos {
+  int x, y, z;
+};
+__device__ __forceinline__ GridPos XcdEntryMajor() {
+  const int X = gridDim.x, subs = X * gridDim.z;
+  const int L = blockIdx.x + X * (blockIdx.y + gridDim.y * blockIdx.z);
+  const int k = L >> 3, sub = k % subs;
+  return {sub % X, 8 * (k / subs) + (L & 7), sub / X};
+}
+
 template <int K2, int CB, int NRBT, int CPWV>
-__global__ void __launch_bounds__(256) Exl3GemmPrefill2Kernel(GemmArgs g) {
+__global__ void __launch_bounds__(256) Exl3GemmPrefillKernel(GemmArgs g) {
   constexpr int T = TileDwords(K2);
   constexpr int SD = 4 * T;
   constexpr int DPL = (SD + 63) / 64;
@@ -452,11 +283,12 @@ __global__ void __launch_bounds__(256) Exl3GemmPrefill2Kernel(GemmArgs g) {
   __shared__ __align__(16) char smem[XBYTES > EBYTES ? XBYTES : EBYTES];
   __half(*xs)[R][XS] = reinterpret_cast<__half(*)[R][XS]>(smem);
   const int n_entries = g.n_entries ? *g.n_entries : g.n_entries_host;
-  const int ei = (int)blockIdx.y + g.entry_base;
+  const GridPos gp = XcdEntryMajor();
+  const int ei = gp.y + g.entry_base;
   if (ei >= n_entries) return;
   const int4 ent = g.entries[ei];
-  const GemmPlane& pl = g.plane[blockIdx.z];
-  const int cpg = blockIdx.x;
+  const GemmPlane& pl = g.plane[gp.z];
+  const int cpg = gp.x;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int steps = g.A / 2;
   const int row0 = ent.y, nrows = ent.z;

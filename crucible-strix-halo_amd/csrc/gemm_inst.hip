@@ -42,31 +42,11 @@ bool CX_CAT(LaunchGemmRate, CX_RATE)(int cb, int nrb, int ksw, dim3 grid, const 
   return false;
 }
 
-bool CX_CAT(LaunchGemmPrefillRate, CX_RATE)(int cb, int nrb, dim3 grid, const GemmArgs& g, hipStream_t s) {
-  constexpr int K2 = CX_RATE;
-  auto go = [&](auto cbc, auto nrbc) {
-    constexpr int CB = decltype(cbc)::value, NRB = decltype(nrbc)::value;
-    hipLaunchKernelGGL((Exl3GemmPrefillKernel<K2, CB, NRB>), grid, dim3(512), 0, s, g);
-    return true;
-  };
-  auto rows = [&](auto cbc) {
-    if (nrb == 4) return go(cbc, IC<4>{});
-    if (nrb == 2) return go(cbc, IC<2>{});
-    return false;
-  };
-  if (cb == kCbMul1) return rows(IC<kCbMul1>{});
-  if constexpr (K2 % 2 == 0) {
-    if (cb == kCbMcg) return rows(IC<kCbMcg>{});
-    if (cb == kCb3Inst) return rows(IC<kCb3Inst>{});
-  }
-  return false;
-}
-
-bool CX_CAT(LaunchGemmPrefill2Rate, CX_RATE)(int cb, int nrbt, int cpwv, dim3 grid, const GemmArgs& g, hipStream_t s) {
+bool CX_CAT(LaunchGemmPrefillRate, CX_RATE)(int cb, int nrbt, int cpwv, dim3 grid, const GemmArgs& g, hipStream_t s) {
   constexpr int K2 = CX_RATE;
   auto go = [&](auto cbc, auto nc, auto cc) {
     constexpr int CB = decltype(cbc)::value, NRBT = decltype(nc)::value, CPWV = decltype(cc)::value;
-    hipLaunchKernelGGL((Exl3GemmPrefill2Kernel<K2, CB, NRBT, CPWV>), grid, dim3(256), 0, s, g);
+    hipLaunchKernelGGL((Exl3GemmPrefillKernel<K2, CB, NRBT, CPWV>), grid, dim3(256), 0, s, g);
     return true;
   };
   auto shape = [&](auto cbc) {

@@ -68,15 +68,12 @@ void FillLinearTables(int4* ent, MatPtr* mat, const LinearPlan& p, int M, const 
 // Launches Exl3GemmKernel for a runtime (rate, codebook, rows per wave, waves per
 // column pair).  Returns false for an unsupported combination.
 bool LaunchGemm(int k2, int cb, int nrb, int ksw, int u, dim3 grid, const GemmArgs& g, hipStream_t s);
-// The decode-once prefill GEMM (Exl3GemmPrefillKernel): grid (O / 128, entries, planes).
-bool LaunchGemmPrefill(int k2, int cb, int nrb, dim3 grid, const GemmArgs& g, hipStream_t s);
-// The register-blocked prefill GEMM (Exl3GemmPrefill2Kernel): grid (O / (128 cpwv), entries, planes).
-bool LaunchGemmPrefill2(int k2, int cb, int nrbt, int cpwv, dim3 grid, const GemmArgs& g, hipStream_t s);
+// The prefill GEMM (Exl3GemmPrefillKernel): grid (O / (128 cpwv), entries padded to 8, planes).
+bool LaunchGemmPrefill(int k2, int cb, int nrbt, int cpwv, dim3 grid, const GemmArgs& g, hipStream_t s);
 // Per-rate launchers (one translation unit per rate, gemm_inst.hip).
 #define CX_DECLARE_RATE(K2)                                                                          \
   bool LaunchGemmRate##K2(int cb, int nrb, int ksw, dim3 grid, const GemmArgs& g, hipStream_t s); \
-  bool LaunchGemmPrefillRate##K2(int cb, int nrb, dim3 grid, const GemmArgs& g, hipStream_t s);   \
-  bool LaunchGemmPrefill2Rate##K2(int cb, int nrbt, int cpwv, dim3 grid, const GemmArgs& g, hipStream_t s);
+  bool LaunchGemmPrefillRate##K2(int cb, int nrbt, int cpwv, dim3 grid, const GemmArgs& g, hipStream_t s);
 CX_DECLARE_RATE(2)
 CX_DECLARE_RATE(3)
 CX_DECLARE_RATE(4)

@@ -364,17 +364,17 @@ struct cx_moe_plan {
 namespace cx {
 
 struct MoeSizes {
-  int M, P, n, nsh, chunk, nrb, cpwv, variant, max_entries, ntiles;
+  int M, P, n, nsh, chunk, nrb, cpwv, max_entries, ntiles;
   bool small, prefill;
   size_t off_sel, off_wts, off_counts, off_offsets, off_pairs, off_rows, off_inv, off_ent, off_nent, off_tiles;
   size_t off_xg, off_xu, off_yg, off_yu, off_xd, off_yd, total;
 };
 
-// Prefill GEMM shape.  Variant 1 (producer / consumer): 4 waves x 16 nrb rows share each
-// decoded tile.  Variant 2 (register-blocked): a workgroup covers 16 nrb rows x 128 cpwv
-// columns.  Environment overrides: CX_PREFILL_KERNEL, CX_PREFILL_NRB, CX_PREFILL_CPWV.
+// Prefill GEMM shape: a workgroup covers 16 nrb rows x 128 cpwv columns (every row of an
+// entry shares each decoded tile).  Environment overrides: CX_PREFILL_NRB (4 | 8),
+// CX_PREFILL_CPWV (1 | 2).
 struct PrefillShape {
-  int variant, nrb, cpwv;
+  int nrb, cpwv;
 };
 PrefillShape PrefillConfig() {
   static const PrefillShape ps = [] {
@@ -382,12 +382,7 @@ PrefillShape PrefillConfig() {
       const char* e = std::getenv(k);
       return e ? std::atoi(e) : d;
     };
-    PrefillShape p{env("CX_PREFILL_KERNEL", 2), 0, 0};
-    if (p.variant != 1) p.variant = 2;
-    const int nrb = env("CX_PREFILL_NRB", p.variant == 1 ? 2 : 4);
-    p.nrb = p.variant == 1 ? (nrb == 4 ? 4 : 2) : (nrb == 8 ? 8 : 4);
-    p.cpwv = p.variant == 1 ? 1 : (env("CX_PREFILL_CPWV", 1) == 2 ? 2 : 1);
-    return p;
+    return PrefillShape{env("CX_PREFILL_NRB", 4) == 8 ? 8 : 4, env("CX_PREFILL_CPWV", 1) == 2 ? 2 : 1};
   }();
   return ps;
 }
@@ -402,9 +397,8 @@ MoeSizes PlanMoe(const cx_moe_plan* pl, int M, int mode) {
   const PrefillShape ps = PrefillConfig();
   s.nrb = decode ? 1 : ps.nrb;
   s.cpwv = decode ? 1 : ps.cpwv;
-  s.variant = decode ? 0 : ps.variant;
   // Decode: one 16-row block per entry; prefill: every row of an entry shares each decoded tile.
-  s.chunk = decode ? 16 : s.variant == 1 ? 64 * s.nrb : 16 * s.nrb;
+  s.chunk = 16 * s.nrb;
   s.nsh = (M + s.chunk - 1) / s.chunk;
   s.max_entries = s.nsh + std::min(pl->E, s.n) + s.n / s.chunk;
   s.small = s.n <= kSmallRoutes;
@@ -481,11 +475,11 @@ bool LaunchExpertGemm(const cx_moe_plan* pl, const MoeSizes& sz, bool gate_up, c
   const int k2r = gate_up ? pl->k2_gu : pl->k2_d, cbr = gate_up ? pl->cb_gu : pl->cb_d;
   const int k2s = gate_up ? pl->k2_sgu : pl->k2_sd, cbs = gate_up ? pl->cb_sgu : pl->cb_sd;
   const int cpwv = g.ncp % (4 * sz.cpwv) == 0 ? sz.cpwv : 1;
-  const int cpg = sz.variant == 2 ? g.ncp / (4 * cpwv) : sz.prefill ? g.ncp / 4 : g.ncp / (4 / ksw);
+  const int cpg = sz.prefill ? g.ncp / (4 * cpwv) : g.ncp / (4 / ksw);
   auto launch = [&](int k2, int cb, int ny) {
-    const dim3 grid(cpg, ny, planes);
-    if (sz.variant == 2) return LaunchGemmPrefill2(k2, cb, sz.nrb, cpwv, grid, g, s);
-    return sz.prefill ? LaunchGemmPrefill(k2, cb, sz.nrb, grid, g, s) : LaunchGemm(k2, cb, sz.nrb, ksw, 4, grid, g, s);
+    if (sz.prefill)  // entry-major XCD placement needs the entry count padded to 8
+      return LaunchGemmPrefill(k2, cb, sz.nrb, cpwv, dim3(cpg, (ny + 7) / 8 * 8, planes), g, s);
+    return LaunchGemm(k2, cb, sz.nrb, ksw, 4, dim3(cpg, ny, planes), g, s);
   };
   if (k2r == k2s && cbr == cbs) {
     g.n_entries = nent;
