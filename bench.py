@@ -49,6 +49,11 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--seed", type=int, default=2024)
+    ap.add_argument("--host-data", action="store_true",
+                    help="generate the layers with numpy on the host (no torch kernels in the process)")
+    ap.add_argument("--calibrate-copy-mib", type=int, default=0,
+                    help="before the timed region, one device-to-device copy of this many MiB "
+                         "(the reference kernel for scaling HBM byte counters)")
     return ap.parse_args()
 
 
@@ -134,9 +139,11 @@ def cpu_baseline(plan, batch, seconds):
     while steps == 0 or elapsed < seconds:
         sel, wts = O.route(lgh, E, TOPK)
         used = sorted(set(sel.ravel().tolist()))
-        raw = {e: {k: (plan._experts[e][k].trellis.cpu().numpy().view(np.uint16), plan._experts[e][k])
-                   for k in ("gate", "up", "down")} for e in used}
-        sh_raw = {k: (plan._shared[k].trellis.cpu().numpy().view(np.uint16), plan._shared[k]) for k in ("gate", "up", "down")}
+        def host(t):
+            return (t.cpu().numpy() if hasattr(t, "cpu") else t).view(np.uint16)
+        raw = {e: {k: (host(plan._experts[e][k].trellis), plan._experts[e][k]) for k in ("gate", "up", "down")}
+               for e in used}
+        sh_raw = {k: (host(plan._shared[k].trellis), plan._shared[k]) for k in ("gate", "up", "down")}
         t1 = time.perf_counter()
         experts = {}
         for e in used:
@@ -175,7 +182,15 @@ def main():
     from exl3moe import CX_MOE_DECODE, CX_MOE_PREFILL, synth
 
     torch.cuda.init()
-    plans = [synth.device_moe_layer(args.seed + i, E=E, H=H, Ie=IE, topk=TOPK) for i in range(args.layers)]
+    make_layer = synth.host_moe_layer if args.host_data else synth.device_moe_layer
+    plans = [make_layer(args.seed + i, E=E, H=H, Ie=IE, topk=TOPK) for i in range(args.layers)]
+    if args.calibrate_copy_mib:
+        n = args.calibrate_copy_mib << 20
+        src = torch.from_numpy(np.ones(n, dtype=np.uint8)).cuda()
+        dst = torch.from_numpy(np.zeros(n, dtype=np.uint8)).cuda()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     k2 = 8
     eb = expert_bytes(k2, k2)
     nb = max(args.steps, 8)

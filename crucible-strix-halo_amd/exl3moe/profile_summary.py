@@ -1,0 +1,117 @@
+"""Summaries of rocprofv3 output for the kernels of this library.
+
+    python -m exl3moe.profile_summary stats DIR OUT.txt --cmd "..."
+        per-kernel time table from a `rocprofv3 --kernel-trace --stats` run (*kernel_stats.csv)
+
+    python -m exl3moe.profile_summary traffic FETCH_DIR WRITE_DIR OUT.json --copy-bytes N
+                                      --kernel SUBSTR --cmd "..."
+        HBM bytes per dispatch of the kernels whose name contains SUBSTR, from one
+        `--pmc FETCH_SIZE` run and one `--pmc WRITE_SIZE` run of the same program.  Both
+        counters are scaled by what they read for a plain device-to-device copy of N bytes
+        in the same run (the blit kernel `__amd_rocclr_copyBuffer*`), so the result is in
+        bytes whatever the counters' sampling covers.
+"""
+from __future__ import annotations
+
+import argparse
+import csv
+import glob
+import json
+import os
+import statistics
+
+
+def _csvs(d: str, suffix: str) -> list[str]:
+    return sorted(glob.glob(os.path.join(d, "**", f"*{suffix}"), recursive=True))
+
+
+def stats(d: str, out: str, cmd: str, top: int = 20) -> None:
+    files = _csvs(d, "kernel_stats.csv")
+    if not files:
+        raise SystemExit(f"no *kernel_stats.csv under {d}")
+    rows = []
+    for f in files:
+        rows += list(csv.DictReader(open(f)))
+    rows.sort(key=lambda r: -float(r["TotalDurationNs"]))
+    total = sum(float(r["TotalDurationNs"]) for r in rows)
+    with open(out, "w") as o:
+        o.write(f"# rocprofv3 kernel statistics\n# command: {cmd}\n")
+        o.write(f"# {'calls':>6} {'avg_us':>10} {'min_us':>9} {'max_us':>9} {'total_ms':>9} {'%':>6}  kernel\n")
+        for r in rows[:top]:
+            o.write(f"  {int(r['Calls']):6d} {float(r['AverageNs']) / 1e3:10.2f} {float(r['MinNs']) / 1e3:9.2f} "
+                    f"{float(r['MaxNs']) / 1e3:9.2f} {float(r['TotalDurationNs']) / 1e6:9.3f} "
+                    f"{100 * float(r['TotalDurationNs']) / total:6.2f}  {r['Name'][:110]}\n")
+
+
+def _counter(d: str, name: str) -> dict[str, list[float]]:
+    """Kernel name -> per-dispatch values of one counter."""
+    out: dict[str, list[float]] = {}
+    files = _csvs(d, "counter_collection.csv")
+    if not files:
+        raise SystemExit(f"no *counter_collection.csv under {d}")
+    for f in files:
+        for r in csv.DictReader(open(f)):
+            if r["Counter_Name"] == name:
+                out.setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]))
+    return out
+
+
+def traffic(fetch_dir: str, write_dir: str, out: str, copy_bytes: int, kernel: str, cmd: str) -> dict:
+    fetch, write = _counter(fetch_dir, "FETCH_SIZE"), _counter(write_dir, "WRITE_SIZE")
+
+    def pick(tab, sub, what):
+        vals = [v for k, vs in tab.items() if sub in k for v in vs]
+        if not vals:
+            raise SystemExit(f"no dispatch of a kernel containing {sub!r} in the {what} run")
+        return vals
+
+    # The copy: the largest dispatch of the blit kernel (smaller blits are torch's uploads).
+    cf = max(pick(fetch, "copyBuffer", "FETCH_SIZE"))
+    cw = max(pick(write, "copyBuffer", "WRITE_SIZE"))
+    f_scale = copy_bytes / 1024.0 / cf
+    w_scale = copy_bytes / 1024.0 / cw
+    kf = pick(fetch, kernel, "FETCH_SIZE")
+    kw = pick(write, kernel, "WRITE_SIZE")
+    fetch_b = statistics.mean(kf) * 1024 * f_scale
+    write_b = statistics.mean(kw) * 1024 * w_scale
+    res = {
+        "kernel": kernel,
+        "command": cmd,
+        "dispatches": {"fetch_run": len(kf), "write_run": len(kw)},
+        "raw_KiB_per_dispatch": {"FETCH_SIZE": statistics.mean(kf), "WRITE_SIZE": statistics.mean(kw)},
+        "copy_calibration": {"bytes": copy_bytes, "FETCH_SIZE_KiB": cf, "WRITE_SIZE_KiB": cw,
+                             "fetch_scale": f_scale, "write_scale": w_scale},
+        "hbm_fetch_bytes_per_launch": round(fetch_b),
+        "hbm_write_bytes_per_launch": round(write_b),
+        "hbm_bytes_per_launch": round(fetch_b + write_b),
+    }
+    with open(out, "w") as o:
+        json.dump(res, o, indent=1)
+        o.write("\n")
+    return res
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    sub = ap.add_subparsers(dest="what", required=True)
+    s = sub.add_parser("stats")
+    s.add_argument("dir")
+    s.add_argument("out")
+    s.add_argument("--cmd", required=True)
+    s.add_argument("--top", type=int, default=20)
+    t = sub.add_parser("traffic")
+    t.add_argument("fetch_dir")
+    t.add_argument("write_dir")
+    t.add_argument("out")
+    t.add_argument("--copy-bytes", type=int, required=True)
+    t.add_argument("--kernel", required=True)
+    t.add_argument("--cmd", required=True)
+    a = ap.parse_args()
+    if a.what == "stats":
+        stats(a.dir, a.out, a.cmd, a.top)
+    else:
+        print(json.dumps(traffic(a.fetch_dir, a.write_dir, a.out, a.copy_bytes, a.kernel, a.cmd)))
+
+
+if __name__ == "__main__":
+    main()

@@ -67,3 +67,23 @@ def device_moe_layer(seed: int, E: int, H: int, Ie: int, topk: int, bits_gu: flo
     experts = [one(bits_gu, bits_d) for _ in range(E)]
     shared = one(sg, sd)
     return MoePlan(H, Ie, experts, shared, topk)
+
+
+def host_moe_layer(seed: int, E: int, H: int, Ie: int, topk: int, bits_gu: float = 4, bits_d: float = 4):
+    """The same kind of layer as device_moe_layer, generated with numpy on the host and
+    uploaded: a process built this way runs no GPU kernels but the library's (and the
+    uploads), which is what counter-collection runs want."""
+    from .ops import DeviceLinear, MoePlan
+    rng = np.random.default_rng(seed)
+
+    def lin(I, O, bits):
+        tr, suh, svh = linear(rng, I, O, bits)
+        d = DeviceLinear.from_trellis(tr.view(np.int16), suh, svh, bits)
+        d.trellis = tr  # checkpoint order, kept on the host for host-side checks
+        return d
+
+    def one():
+        return {"gate": lin(H, Ie, bits_gu), "up": lin(H, Ie, bits_gu), "down": lin(Ie, H, bits_d)}
+
+    experts = [one() for _ in range(E)]
+    return MoePlan(H, Ie, experts, one(), topk)

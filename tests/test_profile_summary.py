@@ -1,0 +1,48 @@
+"""Host logic of exl3moe.profile_summary on synthetic rocprofv3 CSV files."""
+import csv
+import json
+
+from exl3moe import profile_summary as ps
+
+
+def _write(path, rows, fields):
+    path.parent.mkdir(parents=True, exist_ok=True)
+    with open(path, "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=fields)
+        w.writeheader()
+        w.writerows(rows)
+
+
+def test_traffic_scales_by_copy(tmp_path):
+    fields = ["Kernel_Name", "Counter_Name", "Counter_Value"]
+    # Counters that see half of the reads and all of the writes.
+    _write(tmp_path / "f" / "host" / "1" / "run_counter_collection.csv",
+           [{"Kernel_Name": "__amd_rocclr_copyBuffer", "Counter_Name": "FETCH_SIZE", "Counter_Value": 512},
+            {"Kernel_Name": "__amd_rocclr_copyBuffer", "Counter_Name": "FETCH_SIZE", "Counter_Value": 3},
+            {"Kernel_Name": "void cx::K<1>(x)", "Counter_Name": "FETCH_SIZE", "Counter_Value": 100},
+            {"Kernel_Name": "void cx::K<1>(x)", "Counter_Name": "FETCH_SIZE", "Counter_Value": 300},
+            {"Kernel_Name": "void cx::K<2>(x)", "Counter_Name": "FETCH_SIZE", "Counter_Value": 7}], fields)
+    _write(tmp_path / "w" / "run_counter_collection.csv",
+           [{"Kernel_Name": "__amd_rocclr_copyBuffer", "Counter_Name": "WRITE_SIZE", "Counter_Value": 1024},
+            {"Kernel_Name": "void cx::K<1>(x)", "Counter_Name": "WRITE_SIZE", "Counter_Value": 10}], fields)
+    out = tmp_path / "t.json"
+    r = ps.traffic(str(tmp_path / "f"), str(tmp_path / "w"), str(out), 1 << 20, "K<1>", "cmd")
+    assert r["copy_calibration"]["fetch_scale"] == 2.0 and r["copy_calibration"]["write_scale"] == 1.0
+    assert r["hbm_fetch_bytes_per_launch"] == 200 * 1024 * 2
+    assert r["hbm_write_bytes_per_launch"] == 10 * 1024
+    assert json.loads(out.read_text())["hbm_bytes_per_launch"] == 200 * 2048 + 10240
+
+
+def test_stats_table(tmp_path):
+    fields = ["Name", "Calls", "TotalDurationNs", "AverageNs", "Percentage", "MinNs", "MaxNs", "StdDev"]
+    _write(tmp_path / "s" / "bench_kernel_stats.csv",
+           [{"Name": "a", "Calls": 2, "TotalDurationNs": 4000, "AverageNs": 2000, "Percentage": 20, "MinNs": 1000,
+             "MaxNs": 3000, "StdDev": 1},
+            {"Name": "b", "Calls": 1, "TotalDurationNs": 16000, "AverageNs": 16000, "Percentage": 80,
+             "MinNs": 16000, "MaxNs": 16000, "StdDev": 0}], fields)
+    out = tmp_path / "s.txt"
+    ps.stats(str(tmp_path / "s"), str(out), "the command")
+    lines = out.read_text().splitlines()
+    assert lines[1] == "# command: the command"
+    assert lines[3].split()[-1] == "b" and lines[4].split()[-1] == "a"
+    assert lines[4].split()[1] == "2.00"
