@@ -80,14 +80,13 @@ __device__ __forceinline__ uint32_t StateProduct(uint32_t r, uint32_t mult) {
   return HI ? MadU16Hi(r, mult & 0xffffu, t) : MadU16Lo(r, mult & 0xffffu, t);
 }
 
-// Codebook value bits (low 16 bits of the result; high bits are not defined) of the
-// state in the low / high half of r.  mul1: 0x6400 + bytesum(p) is the fp16 encoding
-// of 1024 + bytesum; the affine map is applied later on packed pairs.
+// Per-state codebook term of the state in the low (HI = false) or high half of r.
+// mul1: the 32-bit product p = s * 0x83DCD12D (its byte sum is taken per pair below).
+// mcg / 3inst: the fp16 value bits in the low 16 bits (high bits not defined).
 template <int CB, bool HI>
-__device__ __forceinline__ uint32_t CodeWord(uint32_t r) {
+__device__ __forceinline__ uint32_t CodeTerm(uint32_t r) {
   if constexpr (CB == kCbMul1) {
-    const uint32_t p = StateProduct<HI>(r, 0x83DCD12Du);
-    return __builtin_amdgcn_udot4(p, 0x01010101u, 0x6400u, false);
+    return StateProduct<HI>(r, 0x83DCD12Du);
   } else {
     uint32_t p = StateProduct<HI>(r, CB == kCbMcg ? 0xCBAC1FEDu : 89226354u);
     if constexpr (CB == kCb3Inst) p += 64248484u;
@@ -98,20 +97,25 @@ __device__ __forceinline__ uint32_t CodeWord(uint32_t r) {
   }
 }
 
-// Two code words -> packed fp16 weights (lo = a, hi = b).
+// Two states' terms -> packed fp16 weights (lo = a, hi = b).
+// mul1: 0x6400 + bytesum(p) is the fp16 encoding of 1024 + bytesum.  The byte sums of a
+// and b land directly in the two halves: v_dot4_u32_u8 adds bytesum(a) to 0x64006400
+// (at most 0x67fc, no carry into the high half), v_sad_hi_u8 against zero adds
+// bytesum(b) << 16.  Then the affine map h * 0x1eee + 0xc931 as one fp16 FMA (one
+// rounding, docs/EXL3_FORMAT.md:120-131) on the pair.
 template <int CB>
 __device__ __forceinline__ half2_t PairWeights(uint32_t a, uint32_t b) {
-  const uint32_t packed = __builtin_amdgcn_perm(b, a, 0x05040100u);
-  half2_t h = __builtin_bit_cast(half2_t, packed);
   if constexpr (CB == kCbMul1) {
-    // fp16 FMA with one rounding: h * 0x1eee + 0xc931 (docs/EXL3_FORMAT.md:120-131).
+    uint32_t r = __builtin_amdgcn_udot4(a, 0x01010101u, 0x64006400u, false);
+    r = __builtin_amdgcn_sad_hi_u8(b, 0u, r);
     const half2_t inv = {__builtin_bit_cast(_Float16, (unsigned short)0x1eee),
                          __builtin_bit_cast(_Float16, (unsigned short)0x1eee)};
     const half2_t bias = {__builtin_bit_cast(_Float16, (unsigned short)0xc931),
                           __builtin_bit_cast(_Float16, (unsigned short)0xc931)};
-    h = __builtin_elementwise_fma(h, inv, bias);
+    return __builtin_elementwise_fma(__builtin_bit_cast(half2_t, r), inv, bias);
+  } else {
+    return __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(b, a, 0x05040100u));
   }
-  return h;
 }
 
 // Per-lane constants of the run window.
@@ -157,8 +161,8 @@ __device__ __forceinline__ void DecodeRun(uint32_t w0, uint32_t w1, uint32_t w2,
     for (int j = 0; j < 4; ++j) {
       const int e = RunEnd(K2, j + 4);
       const uint32_t r = e <= 32 ? (a0 >> (32 - e)) : AlignBit(a0, a1, 64 - e);
-      c[j] = CodeWord<CB, true>(r);
-      c[j + 4] = CodeWord<CB, false>(r);
+      c[j] = CodeTerm<CB, true>(r);
+      c[j + 4] = CodeTerm<CB, false>(r);
     }
   } else {
 #pragma unroll
@@ -168,7 +172,7 @@ __device__ __forceinline__ void DecodeRun(uint32_t w0, uint32_t w1, uint32_t w2,
       if (e <= 32) r = a0 >> (32 - e);
       else if (e <= 64) r = AlignBit(a0, a1, 64 - e);
       else r = AlignBit(a1, a2, 96 - e);
-      c[j] = CodeWord<CB, false>(r);
+      c[j] = CodeTerm<CB, false>(r);
     }
   }
   const half2_t p0 = PairWeights<CB>(c[0], c[1]), p1 = PairWeights<CB>(c[2], c[3]);

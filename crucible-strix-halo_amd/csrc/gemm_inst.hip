@@ -12,7 +12,7 @@ namespace cx {
 
 bool CX_CAT(LaunchGemmRate, CX_RATE)(int cb, int nrb, int ksw, dim3 grid, const GemmArgs& g, hipStream_t s) {
   constexpr int K2 = CX_RATE;
-  constexpr int U = 4;
+  constexpr int U = 2;  // step groups in flight per wave (fewer registers, more waves)
   auto go = [&](auto cbc, auto nrbc, auto kswc) {
     constexpr int CB = decltype(cbc)::value, NRB = decltype(nrbc)::value, KSW = decltype(kswc)::value;
     hipLaunchKernelGGL((Exl3GemmKernel<K2, CB, NRB, KSW, U>), grid, dim3(256), 0, s, g);
@@ -38,28 +38,6 @@ bool CX_CAT(LaunchGemmRate, CX_RATE)(int cb, int nrb, int ksw, dim3 grid, const 
     if (nrb != 1 || ksw != 4) return false;
     if (cb == kCbMcg) return go(IC<kCbMcg>{}, IC<1>{}, IC<4>{});
     if (cb == kCb3Inst) return go(IC<kCb3Inst>{}, IC<1>{}, IC<4>{});
-  }
-  return false;
-}
-
-bool CX_CAT(LaunchGemmPrefillRate, CX_RATE)(int cb, int nrbt, int cpwv, dim3 grid, const GemmArgs& g, hipStream_t s) {
-  constexpr int K2 = CX_RATE;
-  auto go = [&](auto cbc, auto nc, auto cc) {
-    constexpr int CB = decltype(cbc)::value, NRBT = decltype(nc)::value, CPWV = decltype(cc)::value;
-    hipLaunchKernelGGL((Exl3GemmPrefillKernel<K2, CB, NRBT, CPWV>), grid, dim3(256), 0, s, g);
-    return true;
-  };
-  auto shape = [&](auto cbc) {
-    if (nrbt == 4 && cpwv == 1) return go(cbc, IC<4>{}, IC<1>{});
-    if (nrbt == 8 && cpwv == 1) return go(cbc, IC<8>{}, IC<1>{});
-    if (nrbt == 4 && cpwv == 2) return go(cbc, IC<4>{}, IC<2>{});
-    if (nrbt == 8 && cpwv == 2) return go(cbc, IC<8>{}, IC<2>{});
-    return false;
-  };
-  if (cb == kCbMul1) return shape(IC<kCbMul1>{});
-  if constexpr (K2 % 2 == 0) {
-    if (cb == kCbMcg) return shape(IC<kCbMcg>{});
-    if (cb == kCb3Inst) return shape(IC<kCb3Inst>{});
   }
   return false;
 }

@@ -1,0 +1,38 @@
+// Exl3GemmPrefillKernel instantiations for one rate (compiled once per rate with
+// -DCX_RATE=K2).  Built with MFMA accumulators in VGPRs (-amdgpu-mfma-vgpr-form): with
+// accumulator VGPRs the register allocator otherwise copies accumulators between the
+// two register files inside the decode loop.
+#include "internal.hpp"
+
+#ifndef CX_RATE
+#error "compile with -DCX_RATE=<2 x bits per weight>"
+#endif
+
+namespace cx {
+
+#define CX_CAT2(a, b) a##b
+#define CX_CAT(a, b) CX_CAT2(a, b)
+
+bool CX_CAT(LaunchGemmPrefillRate, CX_RATE)(int cb, int nrbt, int cpwv, dim3 grid, const GemmArgs& g, hipStream_t s) {
+  constexpr int K2 = CX_RATE;
+  auto go = [&](auto cbc, auto nc, auto cc) {
+    constexpr int CB = decltype(cbc)::value, NRBT = decltype(nc)::value, CPWV = decltype(cc)::value;
+    hipLaunchKernelGGL((Exl3GemmPrefillKernel<K2, CB, NRBT, CPWV>), grid, dim3(256), 0, s, g);
+    return true;
+  };
+  auto shape = [&](auto cbc) {
+    if (nrbt == 4 && cpwv == 1) return go(cbc, IC<4>{}, IC<1>{});
+    if (nrbt == 8 && cpwv == 1) return go(cbc, IC<8>{}, IC<1>{});
+    if (nrbt == 4 && cpwv == 2) return go(cbc, IC<4>{}, IC<2>{});
+    if (nrbt == 8 && cpwv == 2) return go(cbc, IC<8>{}, IC<2>{});
+    return false;
+  };
+  if (cb == kCbMul1) return shape(IC<kCbMul1>{});
+  if constexpr (K2 % 2 == 0) {
+    if (cb == kCbMcg) return shape(IC<kCbMcg>{});
+    if (cb == kCb3Inst) return shape(IC<kCb3Inst>{});
+  }
+  return false;
+}
+
+}  // namespace cx
