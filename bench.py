@@ -8,7 +8,10 @@ Headline workload: 512-expert top-10 MoE layer, hidden 2048,
 intermediate 512, one shared expert, all EXL3 4.0 bpw; 8 ragged sessions of 1..5 rows
 per step (decode).  Weights are read cold: steps rotate over several seeded layers
 (> 2 GiB together, far above the 256 MB Infinity Cache) and every step routes fresh
-logits.  A secondary line measures the 2048-token Zipf-skewed prefill (config 4).
+logits.  Secondary objects in the same line: the 2048-token Zipf-skewed prefill
+(config 4), the ragged EXL3 linear GEMVs (config 2, rotating over 128 seeded weight pairs),
+the 8192-token mixed-rate prefill and 6-bpw output head (config 5), and the measured HBM
+stream rate of a 2 GiB device copy.
 
 Prints ONE JSON line (rank 0).  `value` is decode tokens/s (rows/s through the layer).
 """
@@ -47,6 +50,8 @@ def parse():
     ap.add_argument("--prefill-steps", type=int, default=6)
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-linear", action="store_true", help="skip the config-2 ragged linear measurement")
+    ap.add_argument("--no-long", action="store_true", help="skip the config-5 long prefill + output head")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--seed", type=int, default=2024)
     ap.add_argument("--host-data", action="store_true",
@@ -79,47 +84,189 @@ def make_batches(n, seed, prefill=False):
 
 
 def run_workload(plans, batches, warmup, steps, mode):
-    """Times `steps` layer calls after `warmup`; returns timing, per-step routing and stage times."""
+    """Times `steps` layer calls after `warmup` (no instrumentation in the timed loop), then
+    repeats the same calls with the library's stage events to get per-stage times."""
     import torch
     from exl3moe.trace import StageTrace
     maxM = max(b[0][-1] for b in batches)
     ws = torch.empty(max(p.workspace_size(maxM, mode) for p in plans), dtype=torch.uint8, device="cuda")
     ys = torch.empty(maxM, H, dtype=torch.float32, device="cuda")
     sels = [torch.empty(b[0][-1], TOPK, dtype=torch.int32, device="cuda") for b in batches]
+
+    def call(i):
+        b = i % len(batches)
+        offs, x, lg = batches[b]
+        plans[i % len(plans)](x, lg, row_offsets=offs, mode=mode, workspace=ws, y=ys[:offs[-1]], sel=sels[b])
+        return b
+
     for i in range(warmup):
-        offs, x, lg = batches[i % len(batches)]
-        plans[i % len(plans)](x, lg, row_offsets=offs, mode=mode, workspace=ws, y=ys[:offs[-1]], sel=sels[i % len(batches)])
-    torch.cuda.synchronize()
-    traces = {id(p): StageTrace(p, steps) for p in plans}
-    order = []
+        call(i)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for s in range(steps):
-        b = (warmup + s) % len(batches)
-        offs, x, lg = batches[b]
-        p = plans[s % len(plans)]
-        p(x, lg, row_offsets=offs, mode=mode, workspace=ws, y=ys[:offs[-1]], sel=sels[b])
-        order.append((s % len(plans), b))
+    order = [call(warmup + s) for s in range(steps)]
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    # Stage times per call: each plan's ring holds its own calls in order.
-    ncalls = {id(p): sum(1 for pi, _ in order if plans[pi] is p) for p in plans}
+    # Same calls again with stage events: each plan's ring holds its own calls in order.
+    traces = {id(p): StageTrace(p, steps) for p in plans}
+    for s in range(steps):
+        call(warmup + s)
+    torch.cuda.synchronize()
+    pis = [(warmup + s) % len(plans) for s in range(steps)]
+    ncalls = {id(p): sum(1 for pi in pis if plans[pi] is p) for p in plans}
     per_plan = {id(p): traces[id(p)].stage_ms(ncalls[id(p)]) for p in plans}
     seen = {id(p): 0 for p in plans}
     stage_rows = []
-    for pi, _ in order:
+    for pi in pis:
         pid = id(plans[pi])
         stage_rows.append(per_plan[pid][seen[pid]])
         seen[pid] += 1
     for t in traces.values():
         t.close()
-    rows = sum(batches[b][0][-1] for _, b in order)
-    used = []
-    for _, b in order:
-        sel = sels[b].cpu().numpy()
-        used.append(len(set(sel.ravel().tolist())))
+    rows = sum(batches[b][0][-1] for b in order)
+    used = [len(set(sels[b].cpu().numpy().ravel().tolist())) for b in order]
     return {"wall_s": wall, "rows": rows, "stages": stage_rows, "distinct": used,
-            "M": [batches[b][0][-1] for _, b in order]}
+            "M": [batches[b][0][-1] for b in order]}
+
+
+def pct(v):
+    import numpy as np
+    v = np.asarray(v, dtype=np.float64)
+    return {"p10": round(float(np.percentile(v, 10)), 2), "median": round(float(np.median(v)), 2),
+            "p90": round(float(np.percentile(v, 90)), 2), "mean": round(float(v.mean()), 2)}
+
+
+def stream_peak():
+    """Measured HBM stream rate: device-to-device copies of 2 GiB (read + write bytes / time)."""
+    import torch
+    from exl3moe.trace import EventTimer
+    n = 2 << 30
+    a = torch.empty(n, dtype=torch.uint8, device="cuda")
+    b = torch.empty(n, dtype=torch.uint8, device="cuda")
+    a.fill_(1)
+    b.copy_(a)
+    t = EventTimer(5, torch.cuda.current_stream().cuda_stream)
+    for _ in range(5):
+        t.mark()
+        b.copy_(a)
+    t.mark()
+    ms = t.ms()
+    t.close()
+    del a, b
+    return round(2 * n / (min(ms) / 1000) / 1e9, 1)
+
+
+def bench_linear(seed, copies=128, warmup=10):
+    """Config 2: ragged decode GEMVs 2048->4096 and 4096->2048 at 4 bpw, 8 sessions of 1 + d
+    rows (d ~ U{0..4}), rotating over `copies` seeded weight pairs (> 1 GiB, cold reads)."""
+    import numpy as np
+    import torch
+    from exl3moe import synth
+    from exl3moe.trace import EventTimer
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+    pairs = [(synth.device_linear(gen, 2048, 4096, 4), synth.device_linear(gen, 4096, 2048, 4)) for _ in range(copies)]
+    for a, b in pairs:  # only the repacked tiles are used here
+        a.trellis = b.trellis = None
+    rng = np.random.default_rng(seed)
+    batches = []
+    for _ in range(16):
+        offs = synth.sessions(rng, 8, 1, 5)
+        M = offs[-1]
+        batches.append((offs, torch.from_numpy(rng.standard_normal((M, 2048)).astype(np.float16)).cuda(),
+                        torch.from_numpy(rng.standard_normal((M, 4096)).astype(np.float16)).cuda()))
+    ws = torch.empty(max(pairs[0][0].workspace_size(40), pairs[0][1].workspace_size(40)), dtype=torch.uint8,
+                     device="cuda")
+    y1 = torch.empty(40, 4096, dtype=torch.float32, device="cuda")
+    y2 = torch.empty(40, 2048, dtype=torch.float32, device="cuda")
+
+    def call(i, which):
+        offs, x1, x2 = batches[i % len(batches)]
+        a, b = pairs[i % copies]
+        M = offs[-1]
+        if which == 0:
+            a.forward_into(x1, y1[:M], offs, ws)
+        else:
+            b.forward_into(x2, y2[:M], offs, ws)
+
+    for i in range(warmup):
+        call(i, 0)
+        call(i, 1)
+    torch.cuda.synchronize()
+    t = EventTimer(2 * copies, torch.cuda.current_stream().cuda_stream)
+    for i in range(copies):
+        t.mark()
+        call(warmup + i, 0)
+        t.mark()
+        call(warmup + i, 1)
+    t.mark()
+    ms = np.array(t.ms()).reshape(copies, 2)
+    t.close()
+    out = {"workload": "config2: ragged decode GEMV, 8 sessions x (1 + U{0..4}) rows, EXL3 4.0 bpw, "
+                       f"rotating over {copies} seeded weight pairs", "copies": copies}
+    for j, (I, O) in enumerate(((2048, 4096), (4096, 2048))):
+        Ms = np.array([batches[(warmup + i) % len(batches)][0][-1] for i in range(copies)])
+        by = matrix_bytes(I, O, 8) + Ms * I * 2 + Ms * O * 4
+        gbs = float(by.sum() / (ms[:, j].sum() / 1000)) / 1e9
+        out[f"{I}x{O}"] = {"us": pct(ms[:, j] * 1000), "algorithmic_GBps": round(gbs, 1),
+                           "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+                           "rows_per_s": round(float(Ms.sum() / (ms[:, j].sum() / 1000)), 1)}
+    del pairs
+    torch.cuda.empty_cache()
+    return out
+
+
+def bench_long(seed, steps=3, head_copies=5, head_calls=20):
+    """Config 5: an 8192-token chunk through the layer with gate/up at 3 bpw and down at
+    5 bpw, plus a 6-bpw output head 2048->151936 applied to 4 last-token rows (rotating
+    over `head_copies` seeded heads, > 1 GiB)."""
+    import numpy as np
+    import torch
+    from exl3moe import CX_MOE_PREFILL, synth
+    from exl3moe.trace import EventTimer
+    plan = synth.device_moe_layer(seed, E=E, H=H, Ie=IE, topk=TOPK, bits_gu=3, bits_d=5)
+    rng = np.random.default_rng(seed)
+    M = 8192
+    batch = [([0, M], torch.from_numpy(rng.standard_normal((M, H)).astype(np.float16)).cuda(),
+              torch.from_numpy(rng.standard_normal((M, E + 1)).astype(np.float32)).cuda())]
+    r = run_workload([plan], batch, 1, steps, CX_MOE_PREFILL)
+    del plan
+    ms = r["wall_s"] * 1000 / steps
+    st = np.array(r["stages"])
+    flops = 2.0 * (TOPK + 1) * M * 3 * H * IE
+    out = {"workload": "config5: 8192 tokens, gate/up 3 bpw, down 5 bpw, E=512 top-10 + shared",
+           "tokens_per_s": round(M / (ms / 1000), 1), "ms_per_step": round(ms, 4),
+           "mfma": {"achieved_TFLOPs_layer": round(flops / (ms / 1000) / 1e12, 1), "peak": MFMA_F16_PEAK_TFS,
+                    "frac_layer": round(flops / (ms / 1000) / 1e12 / MFMA_F16_PEAK_TFS, 4)},
+           "stage_us_mean": {n: round(float(st[:, i].mean() * 1000), 2) for i, n in enumerate(
+               ["route", "group", "input", "gate_up", "mid", "down", "combine"])}}
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed + 1)
+    heads = []
+    for _ in range(head_copies):
+        h = synth.device_linear(gen, 2048, 151936, 6)
+        h.trellis = None
+        heads.append(h)
+    x = torch.from_numpy(rng.standard_normal((4, 2048)).astype(np.float16)).cuda()
+    y = torch.empty(4, 151936, dtype=torch.float32, device="cuda")
+    offs = [0, 1, 2, 3, 4]
+    ws = torch.empty(heads[0].workspace_size(4), dtype=torch.uint8, device="cuda")
+    for i in range(head_copies):
+        heads[i].forward_into(x, y, offs, ws)
+    torch.cuda.synchronize()
+    t = EventTimer(head_calls, torch.cuda.current_stream().cuda_stream)
+    for i in range(head_calls):
+        t.mark()
+        heads[i % head_copies].forward_into(x, y, offs, ws)
+    t.mark()
+    hm = np.array(t.ms())
+    t.close()
+    by = matrix_bytes(2048, 151936, 12) + 4 * 2048 * 2 + 4 * 151936 * 4
+    gbs = by / (hm.mean() / 1000) / 1e9
+    out["head"] = {"workload": "EXL3 6.0 bpw 2048->151936 GEMV, 4 rows (one per session)", "copies": head_copies,
+                   "us": pct(hm * 1000), "algorithmic_GBps": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+    del heads
+    torch.cuda.empty_cache()
+    return out
 
 
 def cpu_baseline(plan, batch, seconds):
@@ -237,6 +384,7 @@ def main():
                      "traffic": traffic, "avg_us": round(float(gu.mean() * 1000), 2),
                      "algorithmic_bytes_per_launch": int(gu_bytes.mean())},
         "layer": {"algorithmic_GBps": round(layer_gbs, 1), "frac_hbm": round(layer_gbs / HBM_PEAK_GBS, 4),
+                  "traced_step_us": pct(st.sum(1) * 1000),
                   "stage_us_mean": {n: round(float(st[:, i].mean() * 1000), 2) for i, n in enumerate(
                       ["route", "group", "input", "gate_up", "mid", "down", "combine"])}},
     }
@@ -259,6 +407,11 @@ def main():
             "stage_us_mean": {n: round(float(stp[:, i].mean() * 1000), 2) for i, n in enumerate(
                 ["route", "group", "input", "gate_up", "mid", "down", "combine"])},
         }
+    if not args.no_linear:
+        out["linear"] = bench_linear(args.seed + 300)
+    if not args.no_long:
+        out["prefill_long"] = bench_long(args.seed + 400)
+    out["roofline"]["measured_stream_GBps"] = stream_peak()
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(plans[0], batches[0], args.cpu_seconds)
     print(json.dumps(out), flush=True)

@@ -16,7 +16,44 @@ def hip() -> ctypes.CDLL:
         _hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
         _hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
         _hip.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+        _hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
     return _hip
+
+
+class EventTimer:
+    """Per-call device times of calls issued on one stream (default: the null stream):
+    an event is recorded before each call and after the last."""
+
+    def __init__(self, calls: int, stream=None):
+        self.n = calls + 1
+        self.stream = stream
+        self.events = []
+        for _ in range(self.n):
+            h = ctypes.c_void_p()
+            if hip().hipEventCreate(ctypes.byref(h)) != 0:
+                raise RuntimeError("hipEventCreate failed")
+            self.events.append(h.value)
+        self.i = 0
+
+    def mark(self):
+        if hip().hipEventRecord(self.events[self.i], self.stream) != 0:
+            raise RuntimeError("hipEventRecord failed")
+        self.i += 1
+
+    def ms(self) -> list[float]:
+        hip().hipEventSynchronize(self.events[self.i - 1])
+        t = ctypes.c_float()
+        out = []
+        for a, b in zip(self.events[:self.i - 1], self.events[1:self.i]):
+            if hip().hipEventElapsedTime(ctypes.byref(t), a, b) != 0:
+                raise RuntimeError("hipEventElapsedTime failed")
+            out.append(t.value)
+        return out
+
+    def close(self):
+        for e in self.events:
+            hip().hipEventDestroy(e)
+        self.events = []
 
 
 class StageTrace:
