@@ -71,32 +71,18 @@ struct GemmArgs {
   int S;    // K segments across workgroups
 };
 
-template <int K2, int CB, int NRB, int KSW, int U>
-__global__ void __launch_bounds__(256) Exl3GemmKernel(GemmArgs g) {
-  constexpr int CPW = 4 / KSW;
+// One wave streams `steps` steps of one column pair (tiles from `tiles`, already offset
+// to the wave's first step) against NRB 16-row blocks of MFMA-ordered activations
+// (`x` at the first row, 32 k-columns per step starting at step 0) into acc.
+template <int K2, int CB, int NRB, int U>
+__device__ __forceinline__ void StreamColumnPair(const uint32_t* tiles, int steps, const __half* x, int nrows,
+                                                 int ldx, uint32_t* slot, int lane, float4_t (&acc)[NRB][2]) {
   constexpr int T = TileDwords(K2);    // dwords per tile
   constexpr int SD = 4 * T;            // dwords per step
   constexpr int DPL = (SD + 63) / 64;  // dwords each lane loads per step
   constexpr int ND = WindowDwords(K2);
-  __shared__ uint32_t stage[4][StageDwords<DPL>()];
-  const int n_entries = g.n_entries ? *g.n_entries : g.n_entries_host;
-  const int ei = (int)blockIdx.y + g.entry_base;
-  if (ei >= n_entries) return;
-  const int4 ent = g.entries[ei];
-  const GemmPlane& pl = g.plane[blockIdx.z];
-  const int ncpg = g.ncp / CPW;
-  const int cpg = blockIdx.x % ncpg, kseg = blockIdx.x / ncpg;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  const int cp = cpg * CPW + wave / KSW, ks = wave % KSW;
-  const int nsplit = g.S * KSW, split = kseg * KSW + ks;
-  const int A2 = g.A / 2;
-  const int s0 = A2 * split / nsplit, s1 = A2 * (split + 1) / nsplit;
-  const int steps = s1 - s0, a0 = 2 * s0;
-  const int row0 = ent.y, nrows = ent.z;
-  const MatPtr m = pl.mats[ent.x];
-
-  const __amdgpu_buffer_rsrc_t rw = MakeRsrc(m.tiles + ((size_t)cp * g.A + a0) * 2 * T, (uint32_t)steps * SD * 4);
-  const __amdgpu_buffer_rsrc_t rx = MakeRsrc(pl.x + (size_t)row0 * pl.ldx, (uint32_t)nrows * pl.ldx * 2);
+  const __amdgpu_buffer_rsrc_t rw = MakeRsrc(tiles, (uint32_t)steps * SD * 4);
+  const __amdgpu_buffer_rsrc_t rx = MakeRsrc(x, (uint32_t)nrows * ldx * 2);
   const LaneRun<K2> lr(lane);
   // LDS dword offsets of the lane's windows: run t of tile (k-tile j, column tile tau).
   uint32_t woff[2][ND];
@@ -107,16 +93,14 @@ __global__ void __launch_bounds__(256) Exl3GemmKernel(GemmArgs g) {
   const uint32_t loff = (uint32_t)lane * DPL * 4;
   uint32_t xoff[NRB];
 #pragma unroll
-  for (int rb = 0; rb < NRB; ++rb) xoff[rb] = (uint32_t)(((rb * 16 + (lane & 15)) * pl.ldx + a0 * 16 + 8 * (lane >> 4)) * 2);
-  uint32_t* slot = stage[wave];
+  for (int rb = 0; rb < NRB; ++rb) xoff[rb] = (uint32_t)(((rb * 16 + (lane & 15)) * ldx + 8 * (lane >> 4)) * 2);
 
-  float4_t acc[NRB][2];
 #pragma unroll
   for (int rb = 0; rb < NRB; ++rb) acc[rb][0] = acc[rb][1] = float4_t{0.f, 0.f, 0.f, 0.f};
 
   auto load_w = [&](int s) { return BufLoadN<DPL>(rw, loff, (uint32_t)s * SD * 4); };
   auto load_x = [&](int s, int rb) { return BufLoad128(rx, xoff[rb], (uint32_t)s * 64); };
-  auto step = [&](const Dwords<DPL>& w, const u32x4_t (&x)[NRB]) {
+  auto step = [&](const Dwords<DPL>& w, const u32x4_t (&xv)[NRB]) {
     // Stage the step in the wave's slot; LDS executes a wave's operations in order, so
     // the window reads below see these writes and the next step's writes follow them.
     StageWrite<DPL>(slot, lane, w.v);
@@ -136,7 +120,7 @@ __global__ void __launch_bounds__(256) Exl3GemmKernel(GemmArgs g) {
     const half8_t b1 = {hi0[0], hi0[1], hi0[2], hi0[3], hi1[0], hi1[1], hi1[2], hi1[3]};
 #pragma unroll
     for (int rb = 0; rb < NRB; ++rb) {
-      const half8_t av = __builtin_bit_cast(half8_t, x[rb]);
+      const half8_t av = __builtin_bit_cast(half8_t, xv[rb]);
       acc[rb][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b0, acc[rb][0], 0, 0, 0);
       acc[rb][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b1, acc[rb][1], 0, 0, 0);
     }
@@ -146,12 +130,12 @@ __global__ void __launch_bounds__(256) Exl3GemmKernel(GemmArgs g) {
   // current U steps are decoded; then the remaining (< U) steps one at a time.
   Dwords<DPL> wa[U], wb[U];
   u32x4_t xa[U][NRB], xb[U][NRB];
-  auto load_group = [&](Dwords<DPL> (&w)[U], u32x4_t (&x)[U][NRB], int sb) {
+  auto load_group = [&](Dwords<DPL> (&w)[U], u32x4_t (&xg)[U][NRB], int sb) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       w[u] = load_w(sb + u);
 #pragma unroll
-      for (int rb = 0; rb < NRB; ++rb) x[u][rb] = load_x(sb + u, rb);
+      for (int rb = 0; rb < NRB; ++rb) xg[u][rb] = load_x(sb + u, rb);
     }
   };
   int s = 0;
@@ -177,6 +161,32 @@ __global__ void __launch_bounds__(256) Exl3GemmKernel(GemmArgs g) {
     for (int rb = 0; rb < NRB; ++rb) x1[rb] = load_x(s, rb);
     step(w1, x1);
   }
+}
+
+template <int K2, int CB, int NRB, int KSW, int U>
+__global__ void __launch_bounds__(256) Exl3GemmKernel(GemmArgs g) {
+  constexpr int CPW = 4 / KSW;
+  constexpr int T = TileDwords(K2);
+  constexpr int DPL = (4 * T + 63) / 64;
+  __shared__ uint32_t stage[4][StageDwords<DPL>()];
+  const int n_entries = g.n_entries ? *g.n_entries : g.n_entries_host;
+  const int ei = (int)blockIdx.y + g.entry_base;
+  if (ei >= n_entries) return;
+  const int4 ent = g.entries[ei];
+  const GemmPlane& pl = g.plane[blockIdx.z];
+  const int ncpg = g.ncp / CPW;
+  const int cpg = blockIdx.x % ncpg, kseg = blockIdx.x / ncpg;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int cp = cpg * CPW + wave / KSW, ks = wave % KSW;
+  const int nsplit = g.S * KSW, split = kseg * KSW + ks;
+  const int A2 = g.A / 2;
+  const int s0 = A2 * split / nsplit, s1 = A2 * (split + 1) / nsplit;
+  const int steps = s1 - s0, a0 = 2 * s0;
+  const int row0 = ent.y, nrows = ent.z;
+  const MatPtr m = pl.mats[ent.x];
+  float4_t acc[NRB][2];
+  StreamColumnPair<K2, CB, NRB, U>(m.tiles + ((size_t)cp * g.A + a0) * 2 * T, steps,
+                                   pl.x + (size_t)row0 * pl.ldx + a0 * 16, nrows, pl.ldx, stage[wave], lane, acc);
 
   if constexpr (KSW > 1) {
     // Fixed-order reduction of the K splits of each column pair.
@@ -249,12 +259,6 @@ __global__ void __launch_bounds__(256) Exl3GemmKernel(GemmArgs g) {
 
 namespace cx {
 
-// Prefill GEMM (register-blocked): a workgroup = 4 waves owns 4 CPWV column pairs
-// (128 CPWV columns) x up to 16 NRBT rows of one expert, full K.  Each wave decodes its
-// own CPWV column pairs (B fragments stay in registers, every tile decoded once per
-// workgroup) and multiplies them with all the workgroup's row blocks; the activation
-// tile of a step (16 NRBT rows x 32 inputs) is loaded once into LDS and shared by the 4
-// waves.  One barrier per step double-buffers the activation tile.
 // Workgroups go to the 8 XCDs round-robin by linear id.  This remap puts all gridDim.x *
 // gridDim.z workgroups of row entry y on XCD y % 8, consecutively, so an entry's activation
 // rows are fetched into one L2 and reused there.  gridDim.y must be a multiple of 8.
@@ -268,6 +272,12 @@ __device__ __forceinline__ GridPos XcdEntryMajor() {
   return {sub % X, 8 * (k / subs) + (L & 7), sub / X};
 }
 
+// Prefill GEMM (register-blocked): a workgroup = 4 waves owns 4 CPWV column pairs
+// (128 CPWV columns) x up to 16 NRBT rows of one expert, full K.  Each wave decodes its
+// own CPWV column pairs (B fragments stay in registers, every tile decoded once per
+// workgroup) and multiplies them with all the workgroup's row blocks; the activation
+// tile of a step (16 NRBT rows x 32 inputs) is loaded once into LDS and shared by the 4
+// waves.  One barrier per step double-buffers the activation tile.
 template <int K2, int CB, int NRBT, int CPWV>
 __global__ void __launch_bounds__(256) Exl3GemmPrefillKernel(GemmArgs g) {
   constexpr int T = TileDwords(K2);
