@@ -323,12 +323,23 @@ __global__ void __launch_bounds__(256) MoeMidKernel(const float* __restrict__ yg
   StorePerm32x8(xd + (size_t)p * I + blk * 128, v, kHadNorm);
 }
 
+// Residual write-back of the combine (hyper-connection streams): H row r, stream s at
+// H + r * ldh + s * hidden gets H += post[r][s] * y[r].
+struct HcArgs {
+  const float* post;  // [M][n_streams]
+  float* H;
+  long long ldh;
+  int n_streams;
+};
+
 // Combine: per row, slots 0..topk-1 in selection order then the shared expert:
 // y += w_k * d_k, fp32, where d_k = WHT(y_h) * (norm * svh) came out of the down GEMM's
-// epilogue.  engine/layers/moe_rows.h:634-682.
+// epilogue.  engine/layers/moe_rows.h:634-682.  HC: accumulate into the residual streams
+// instead of storing y (engine/layers/moe_rows.h:672-681).
+template <bool HC>
 __global__ void __launch_bounds__(256) MoeCombineKernel(const float* __restrict__ pd, const float* __restrict__ wts,
                                                         const int* __restrict__ inv, int M, int topk, int H,
-                                                        float* __restrict__ y) {
+                                                        float* __restrict__ y, HcArgs hc) {
   const int nq = H / 4;
   const int item = blockIdx.x * blockDim.x + threadIdx.x;
   if (item >= M * nq) return;
@@ -344,7 +355,20 @@ __global__ void __launch_bounds__(256) MoeCombineKernel(const float* __restrict_
     acc.z += w * d.z;
     acc.w += w * d.w;
   }
-  *reinterpret_cast<float4*>(y + (size_t)r * H + c0) = acc;
+  if constexpr (HC) {
+    for (int st = 0; st < hc.n_streams; ++st) {
+      const float g = hc.post[(size_t)r * hc.n_streams + st];
+      float4* h = reinterpret_cast<float4*>(hc.H + (size_t)r * hc.ldh + (size_t)st * H + c0);
+      float4 v = *h;
+      v.x += g * acc.x;
+      v.y += g * acc.y;
+      v.z += g * acc.z;
+      v.w += g * acc.w;
+      *h = v;
+    }
+  } else {
+    *reinterpret_cast<float4*>(y + (size_t)r * H + c0) = acc;
+  }
 }
 
 }  // namespace cx
@@ -608,11 +632,14 @@ size_t cx_moe_layer_workspace_size(const cx_moe_plan* plan, int32_t M, int32_t m
   return PlanMoe(plan, M, mode).total;
 }
 
-int cx_moe_layer_forward(const cx_moe_plan* pl, const uint16_t* x, const float* logits, int32_t ld,
-                         const float* shared_logit, int32_t M, const int32_t* row_offsets, int32_t n_sessions, float* y,
-                         int32_t* sel_out, float* wts_out, int32_t mode, void* workspace, size_t workspace_bytes,
-                         cx_stream_t stream) {
-  if (!pl || !x || !logits || !y || !workspace) return CX_E_ARG;
+}  // extern "C"
+
+namespace cx {
+
+int MoeForward(const cx_moe_plan* pl, const uint16_t* x, const float* logits, int32_t ld, const float* shared_logit,
+               int32_t M, const int32_t* row_offsets, int32_t n_sessions, float* y, const HcArgs* hc, int32_t* sel_out,
+               float* wts_out, int32_t mode, void* workspace, size_t workspace_bytes, cx_stream_t stream) {
+  if (!pl || !x || !logits || (!y && !hc) || !workspace) return CX_E_ARG;
   if (mode < CX_MOE_AUTO || mode > CX_MOE_PREFILL) return CX_E_ARG;
   if (M <= 0) return CX_E_SHAPE;
   if (ld < pl->E || (!shared_logit && ld < pl->E + 1)) return CX_E_SHAPE;
@@ -670,11 +697,39 @@ int cx_moe_layer_forward(const cx_moe_plan* pl, const uint16_t* x, const float* 
   mark();
   {
     const long items = (long)M * (pl->H / 4);
-    hipLaunchKernelGGL(MoeCombineKernel, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, s, yd, wts, inv, M,
-                       pl->topk, pl->H, y);
+    if (hc)
+      hipLaunchKernelGGL(MoeCombineKernel<true>, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, s, yd, wts, inv,
+                         M, pl->topk, pl->H, nullptr, *hc);
+    else
+      hipLaunchKernelGGL(MoeCombineKernel<false>, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, s, yd, wts, inv,
+                         M, pl->topk, pl->H, y, HcArgs{});
   }
   mark();
   return LaunchStatus();
+}
+
+}  // namespace cx
+
+extern "C" {
+
+int cx_moe_layer_forward(const cx_moe_plan* pl, const uint16_t* x, const float* logits, int32_t ld,
+                         const float* shared_logit, int32_t M, const int32_t* row_offsets, int32_t n_sessions, float* y,
+                         int32_t* sel, float* wts, int32_t mode, void* workspace, size_t workspace_bytes,
+                         cx_stream_t stream) {
+  if (!y) return CX_E_ARG;
+  return MoeForward(pl, x, logits, ld, shared_logit, M, row_offsets, n_sessions, y, nullptr, sel, wts, mode, workspace,
+                    workspace_bytes, stream);
+}
+
+int cx_moe_layer_forward_hc(const cx_moe_plan* pl, const uint16_t* x, const float* logits, int32_t ld,
+                            const float* shared_logit, int32_t M, const int32_t* row_offsets, int32_t n_sessions,
+                            const float* post, int32_t n_streams, float* H, int64_t ldh, int32_t* sel, float* wts,
+                            int32_t mode, void* workspace, size_t workspace_bytes, cx_stream_t stream) {
+  if (!pl || !post || !H) return CX_E_ARG;
+  if (n_streams < 1 || n_streams > 64 || ldh < (int64_t)n_streams * pl->H) return CX_E_SHAPE;
+  const HcArgs hc{post, H, (long long)ldh, n_streams};
+  return MoeForward(pl, x, logits, ld, shared_logit, M, row_offsets, n_sessions, nullptr, &hc, sel, wts, mode,
+                    workspace, workspace_bytes, stream);
 }
 
 int cx_moe_plan_set_trace(cx_moe_plan* plan, void* const* events, int32_t n_events) {

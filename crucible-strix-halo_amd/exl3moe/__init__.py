@@ -22,7 +22,8 @@ ERRORS = {-1: "invalid argument", -2: "invalid shape", -3: "unsupported bitrate"
 EXPORTED = [
     "cx_exl3_tile_bytes", "cx_exl3_repack", "cx_exl3_dequant", "cx_exl3_linear_workspace_size", "cx_exl3_linear",
     "cx_moe_route", "cx_moe_group_workspace_size", "cx_moe_group", "cx_moe_plan_create", "cx_moe_plan_destroy",
-    "cx_moe_layer_workspace_size", "cx_moe_layer_forward", "cx_moe_plan_set_trace", "cx_version",
+    "cx_moe_layer_workspace_size", "cx_moe_layer_forward", "cx_moe_layer_forward_hc", "cx_moe_plan_set_trace",
+    "cx_version",
 ]
 
 
@@ -74,11 +75,13 @@ def lib() -> ctypes.CDLL:
         L.cx_moe_layer_workspace_size.argtypes = [P, I32, I32]
         L.cx_moe_layer_workspace_size.restype = SZ
         L.cx_moe_layer_forward.argtypes = [P, P, P, I32, P, I32, P, I32, P, P, P, I32, P, SZ, P]
+        L.cx_moe_layer_forward_hc.argtypes = [P, P, P, I32, P, I32, P, I32, P, I32, P, ctypes.c_int64, P, P, I32, P,
+                                              SZ, P]
         L.cx_moe_plan_set_trace.argtypes = [P, ctypes.POINTER(ctypes.c_void_p), I32]
         L.cx_moe_plan_set_trace.restype = ctypes.c_int
         L.cx_version.restype = ctypes.c_char_p
         for fn in ("cx_exl3_repack", "cx_exl3_dequant", "cx_exl3_linear", "cx_moe_route", "cx_moe_group",
-                   "cx_moe_plan_create", "cx_moe_layer_forward"):
+                   "cx_moe_plan_create", "cx_moe_layer_forward", "cx_moe_layer_forward_hc"):
             getattr(L, fn).restype = ctypes.c_int
         _lib = L
     return _lib

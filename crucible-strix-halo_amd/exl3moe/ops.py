@@ -134,3 +134,24 @@ class MoePlan:
             self.handle, ptr(x), ptr(logits), logits.shape[1], ptr(shared_logit), M, ro, ns, ptr(y), ptr(sel),
             ptr(wts), mode, ptr(workspace), workspace.numel(), stream_ptr(stream)))
         return y
+
+    def forward_hc(self, x: torch.Tensor, logits: torch.Tensor, post: torch.Tensor, H: torch.Tensor,
+                   shared_logit: torch.Tensor | None = None, row_offsets=None, mode: int = CX_MOE_AUTO,
+                   workspace=None, sel=None, wts=None, stream=None) -> torch.Tensor:
+        """The layer with the residual write-back: H[r, s, :] += post[r, s] * y[r, :] for
+        H of shape [M, n_streams, hidden] (or [M, ldh] with ldh >= n_streams * hidden)."""
+        M = x.shape[0]
+        assert x.dtype == torch.float16 and x.is_contiguous() and x.shape[1] == self.hidden
+        assert logits.dtype == torch.float32 and logits.is_contiguous()
+        assert post.dtype == torch.float32 and post.is_contiguous() and post.shape[0] == M
+        assert H.dtype == torch.float32 and H.shape[0] == M and H.stride(-1) == 1
+        n_streams = post.shape[1]
+        ldh = H.stride(0)
+        if workspace is None:
+            workspace = torch.empty(self.workspace_size(M, mode), dtype=torch.uint8, device=x.device)
+        ro = i32_host(row_offsets)
+        ns = 0 if row_offsets is None else len(row_offsets) - 1
+        check("cx_moe_layer_forward_hc", lib().cx_moe_layer_forward_hc(
+            self.handle, ptr(x), ptr(logits), logits.shape[1], ptr(shared_logit), M, ro, ns, ptr(post), n_streams,
+            ptr(H), ldh, ptr(sel), ptr(wts), mode, ptr(workspace), workspace.numel(), stream_ptr(stream)))
+        return H

@@ -138,6 +138,17 @@ int cx_moe_layer_forward(const cx_moe_plan* plan, const uint16_t* x, const float
                  const float* shared_logit, int32_t M, const int32_t* row_offsets, int32_t n_sessions, float* y,
                  int32_t* sel, float* wts, int32_t mode, void* workspace, size_t workspace_bytes, cx_stream_t stream);
 
+/* The same layer with the reference's residual write-back in place of storing y:
+ * H[r][s][c] += post[r][s] * y[r][c] for the n_streams hyper-connection streams of row r
+ * (H row r at H + r * ldh, stream s at + s * H-width; ldh >= n_streams * hidden), fp32.
+ * Replaces the combine's write-back in MoeRowsCombineKernel (engine/layers/moe_rows.h:
+ * 672-681) and PrefillMoeCombineKernel (engine/layers/prefill_moe.h:670-679).
+ *   post          fp32 [M][n_streams] */
+int cx_moe_layer_forward_hc(const cx_moe_plan* plan, const uint16_t* x, const float* logits, int32_t ld,
+                            const float* shared_logit, int32_t M, const int32_t* row_offsets, int32_t n_sessions,
+                            const float* post, int32_t n_streams, float* H, int64_t ldh, int32_t* sel, float* wts,
+                            int32_t mode, void* workspace, size_t workspace_bytes, cx_stream_t stream);
+
 /* Stage tracing (the reference's per-stage hipEvent marks, engine/engine.hip:2086-2095,
  * stages named at engine/engine.hip:1349-1363).  With n_events > 0 every
  * cx_moe_layer_forward records CX_MOE_TRACE_MARKS events on its stream, into the caller's

@@ -179,3 +179,39 @@ def test_config4_prefill_subset(ops, layer512):
     # which the fp16 rounding points of the mid step can amplify to ~1e-4 at most.
     y2, _, _ = run_layer(layer512, x[:40], lg[:40], 1)
     assert rel_l2(y2, y[:40]) <= 2e-4
+
+
+@pytest.mark.parametrize("mode", [1, 2])
+def test_hc_writeback(ops, mode):
+    # H[r, s] += post[r, s] * y[r] over 4 streams, in a strided H (ldh > 4 * hidden);
+    # y from the plain forward on the same inputs (the layer computation is shared, so y
+    # is bitwise the same; the write-back is one fp32 multiply-add per element).
+    from exl3moe import synth
+    plan = synth.device_moe_layer(13, E=16, H=256, Ie=128, topk=4)
+    rng = np.random.default_rng(3)
+    M, S, ldh = 37, 4, 4 * 256 + 64
+    x = torch.from_numpy(rng.standard_normal((M, 256)).astype(np.float16)).cuda()
+    lg = torch.from_numpy(rng.standard_normal((M, 17)).astype(np.float32)).cuda()
+    post = torch.from_numpy(rng.standard_normal((M, S)).astype(np.float32)).cuda()
+    H0 = rng.standard_normal((M, ldh)).astype(np.float32)
+    Hd = torch.from_numpy(H0.copy()).cuda()
+    y = plan(x, lg, mode=mode).cpu().numpy()
+    plan.forward_hc(x, lg, post, Hd, mode=mode)
+    got = Hd.cpu().numpy()
+    exp = H0.copy()
+    p = post.cpu().numpy()
+    for s in range(S):
+        exp[:, s * 256:(s + 1) * 256] += p[:, s:s + 1] * y
+    np.testing.assert_allclose(got, exp, rtol=0, atol=1e-5 * float(np.abs(exp).max()))
+    np.testing.assert_array_equal(got[:, S * 256:], H0[:, S * 256:])  # padding untouched
+
+
+def test_hc_errors(ops):
+    from exl3moe import CxError, synth
+    plan = synth.device_moe_layer(13, E=16, H=256, Ie=128, topk=4)
+    x = torch.zeros(2, 256, dtype=torch.float16, device="cuda")
+    lg = torch.zeros(2, 17, dtype=torch.float32, device="cuda")
+    post = torch.zeros(2, 4, dtype=torch.float32, device="cuda")
+    with pytest.raises(CxError) as e:
+        plan.forward_hc(x, lg, post, torch.zeros(2, 3 * 256, device="cuda"))  # ldh < 4 * hidden
+    assert e.value.rc == -2
