@@ -21,7 +21,7 @@ ERRORS = {-1: "invalid argument", -2: "invalid shape", -3: "unsupported bitrate"
 
 EXPORTED = [
     "cx_exl3_tile_bytes", "cx_exl3_repack", "cx_exl3_dequant", "cx_exl3_linear_workspace_size", "cx_exl3_linear",
-    "cx_moe_route", "cx_moe_group_workspace_size", "cx_moe_group", "cx_moe_plan_create", "cx_moe_plan_destroy",
+    "cx_dense_linear", "cx_moe_route", "cx_moe_group_workspace_size", "cx_moe_group", "cx_moe_plan_create", "cx_moe_plan_destroy",
     "cx_moe_layer_workspace_size", "cx_moe_layer_forward", "cx_moe_layer_forward_hc", "cx_moe_plan_set_trace",
     "cx_version",
 ]
@@ -65,6 +65,7 @@ def lib() -> ctypes.CDLL:
         L.cx_exl3_linear_workspace_size.argtypes = [ctypes.POINTER(Matrix), I32]
         L.cx_exl3_linear_workspace_size.restype = SZ
         L.cx_exl3_linear.argtypes = [ctypes.POINTER(Matrix), P, I32, P, I32, P, I32, P, SZ, P]
+        L.cx_dense_linear.argtypes = [P, I32, I32, P, I32, I32, I32, P, I32, P]
         L.cx_moe_route.argtypes = [P, I32, I32, I32, I32, P, P, P, P]
         L.cx_moe_group_workspace_size.argtypes = [I32, I32, I32]
         L.cx_moe_group_workspace_size.restype = SZ
@@ -80,7 +81,7 @@ def lib() -> ctypes.CDLL:
         L.cx_moe_plan_set_trace.argtypes = [P, ctypes.POINTER(ctypes.c_void_p), I32]
         L.cx_moe_plan_set_trace.restype = ctypes.c_int
         L.cx_version.restype = ctypes.c_char_p
-        for fn in ("cx_exl3_repack", "cx_exl3_dequant", "cx_exl3_linear", "cx_moe_route", "cx_moe_group",
+        for fn in ("cx_exl3_repack", "cx_exl3_dequant", "cx_exl3_linear", "cx_dense_linear", "cx_moe_route", "cx_moe_group",
                    "cx_moe_plan_create", "cx_moe_layer_forward", "cx_moe_layer_forward_hc"):
             getattr(L, fn).restype = ctypes.c_int
         _lib = L

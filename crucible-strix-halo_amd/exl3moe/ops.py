@@ -73,6 +73,20 @@ class DeviceLinear:
         return y
 
 
+def dense_linear(W: torch.Tensor, x: torch.Tensor, y: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """y = x @ W^T for fp16 W [O][I] and fp32 or fp16 x [M][I] (the router GEMV), fp32 y."""
+    O, I = W.shape
+    M = x.shape[0]
+    assert W.dtype == torch.float16 and W.is_contiguous() and x.shape[1] == I and x.stride(1) == 1
+    assert x.dtype in (torch.float16, torch.float32)
+    if y is None:
+        y = torch.empty(M, O, dtype=torch.float32, device=x.device)
+    xd = CX_F16 if x.dtype == torch.float16 else CX_F32
+    check("cx_dense_linear", lib().cx_dense_linear(ptr(W), O, I, ptr(x), xd, x.stride(0), M, ptr(y), y.stride(0),
+                                                   stream_ptr(stream)))
+    return y
+
+
 def route(logits: torch.Tensor, E: int, topk: int, shared_logit: torch.Tensor | None = None, stream=None):
     M, ld = logits.shape
     sel = torch.empty(M, topk, dtype=torch.int32, device=logits.device)

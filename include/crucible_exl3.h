@@ -104,6 +104,17 @@ typedef struct cx_moe_expert {
   cx_exl3_matrix gate, up, down;
 } cx_moe_expert;
 
+/* Dense fp16-weight linear y[r][o] = W[o] . x[r] for r < M, o < O: the MoE router
+ * (W = [E + 1][H], the shared-expert gate logit as output E).  Replaces LaunchDense
+ * (engine/engine.hip:1824-1870) over DenseGemvKernel (engine/layers/ops.h:30-61) and the
+ * prefill dense kernels.  Up to 8 rows of fp32 x: fp32 products and sums; otherwise x is
+ * rounded to fp16 (as the reference packs it) and multiplied on MFMA with fp32 sums.
+ *   W   fp16 [O][I] row-major, I a multiple of 32
+ *   x   x_dtype CX_F32 / CX_F16, [M][ldx]   (fp32 rows 16-byte aligned: ldx % 4 == 0)
+ *   y   fp32 [M][ldy] */
+int cx_dense_linear(const uint16_t* W, int32_t O, int32_t I, const void* x, int32_t x_dtype, int32_t ldx, int32_t M,
+                    float* y, int32_t ldy, cx_stream_t stream);
+
 /* One MoE layer.  `experts` is a HOST array of E routed experts; the shared expert is
  * always on (slot topk).  Every routed expert must share the gate/up and the down
  * bitrate and codebook (the shared expert may differ).  Replaces `Moe`
