@@ -17,19 +17,23 @@ CX_CB = {"3inst": 0, "mcg": 1, "mul1": 2}
 CX_F16, CX_F32 = 0, 1
 CX_MOE_AUTO, CX_MOE_DECODE, CX_MOE_PREFILL = 0, 1, 2
 ERRORS = {-1: "invalid argument", -2: "invalid shape", -3: "unsupported bitrate", -4: "workspace too small",
-          -5: "expert id out of range", -6: "unsupported combination"}
+          -5: "expert id out of range", -6: "unsupported combination", -7: "checkpoint format error"}
 
 EXPORTED = [
     "cx_exl3_tile_bytes", "cx_exl3_repack", "cx_exl3_dequant", "cx_exl3_linear_workspace_size", "cx_exl3_linear",
     "cx_dense_linear", "cx_moe_route", "cx_moe_group_workspace_size", "cx_moe_group", "cx_moe_plan_create", "cx_moe_plan_destroy",
     "cx_moe_layer_workspace_size", "cx_moe_layer_forward", "cx_moe_layer_forward_hc", "cx_moe_plan_set_trace",
-    "cx_version",
+    "cx_checkpoint_open", "cx_checkpoint_close", "cx_checkpoint_count", "cx_checkpoint_name", "cx_checkpoint_tensor",
+    "cx_exl3_linear_info", "cx_exl3_load_linear", "cx_last_error", "cx_version",
 ]
 
 
 class CxError(RuntimeError):
     def __init__(self, fn: str, rc: int):
-        super().__init__(f"{fn} failed: {ERRORS.get(rc, f'HIP error {rc}')} ({rc})")
+        detail = ""
+        if rc == -7 and _lib is not None:
+            detail = ": " + _lib.cx_last_error().decode(errors="replace")
+        super().__init__(f"{fn} failed: {ERRORS.get(rc, f'HIP error {rc}')} ({rc}){detail}")
         self.rc = rc
 
 
@@ -80,9 +84,23 @@ def lib() -> ctypes.CDLL:
                                               SZ, P]
         L.cx_moe_plan_set_trace.argtypes = [P, ctypes.POINTER(ctypes.c_void_p), I32]
         L.cx_moe_plan_set_trace.restype = ctypes.c_int
+        I64P = ctypes.POINTER(ctypes.c_int64)
+        L.cx_checkpoint_open.argtypes = [ctypes.c_char_p, ctypes.POINTER(ctypes.c_void_p)]
+        L.cx_checkpoint_close.argtypes = [P]
+        L.cx_checkpoint_close.restype = None
+        L.cx_checkpoint_count.argtypes = [P]
+        L.cx_checkpoint_count.restype = I32
+        L.cx_checkpoint_name.argtypes = [P, I32]
+        L.cx_checkpoint_name.restype = ctypes.c_char_p
+        L.cx_checkpoint_tensor.argtypes = [P, ctypes.c_char_p, ctypes.POINTER(I32), ctypes.POINTER(I32), I64P,
+                                           ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_uint64)]
+        L.cx_exl3_linear_info.argtypes = [P, ctypes.c_char_p] + [ctypes.POINTER(I32)] * 4
+        L.cx_exl3_load_linear.argtypes = [P, ctypes.c_char_p, ctypes.POINTER(Matrix), P, P, P, P, SZ, P]
+        L.cx_last_error.restype = ctypes.c_char_p
         L.cx_version.restype = ctypes.c_char_p
         for fn in ("cx_exl3_repack", "cx_exl3_dequant", "cx_exl3_linear", "cx_dense_linear", "cx_moe_route", "cx_moe_group",
-                   "cx_moe_plan_create", "cx_moe_layer_forward", "cx_moe_layer_forward_hc"):
+                   "cx_moe_plan_create", "cx_moe_layer_forward", "cx_moe_layer_forward_hc", "cx_checkpoint_open",
+                   "cx_checkpoint_tensor", "cx_exl3_linear_info", "cx_exl3_load_linear"):
             getattr(L, fn).restype = ctypes.c_int
         _lib = L
     return _lib

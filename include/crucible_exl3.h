@@ -31,7 +31,8 @@ enum {
   CX_E_BITRATE = -3,   /* bits per weight not in 1..8 or 1.5 / 2.5 / 3.5 */
   CX_E_WORKSPACE = -4, /* workspace too small */
   CX_E_EXPERT = -5,    /* expert id out of range */
-  CX_E_UNSUPPORTED = -6
+  CX_E_UNSUPPORTED = -6,
+  CX_E_FORMAT = -7     /* checkpoint file or tensor format error (cx_last_error has the reason) */
 };
 
 enum { CX_CB_3INST = 0, CX_CB_MCG = 1, CX_CB_MUL1 = 2 };   /* codebook, docs/EXL3_FORMAT.md §3 */
@@ -168,6 +169,43 @@ int cx_moe_layer_forward_hc(const cx_moe_plan* plan, const uint16_t* x, const fl
  * copy of the handles; n_events = 0 turns tracing off. */
 #define CX_MOE_TRACE_MARKS 8
 int cx_moe_plan_set_trace(cx_moe_plan* plan, void* const* events, int32_t n_events);
+
+/* ---- checkpoints (host) and the EXL3 linear loader -------------------------------------
+ * A checkpoint is one .safetensors file or a directory with model.safetensors.index.json
+ * and its shards; every shard is memory-mapped read-only until cx_checkpoint_close.
+ * Headers are parsed and every tensor is checked when the checkpoint opens (dtype known,
+ * shape x dtype == data_offsets span inside the payload, unique names, shard names plain
+ * file names).  Replaces st::Checkpoint (engine/exl3/safetensors.h) for the expert
+ * weights.  Errors return CX_E_FORMAT with the file, tensor and reason in cx_last_error. */
+enum {
+  CX_DT_BOOL = 0, CX_DT_U8 = 1, CX_DT_I8 = 2, CX_DT_I16 = 3, CX_DT_U16 = 4, CX_DT_F16 = 5, CX_DT_BF16 = 6,
+  CX_DT_I32 = 7, CX_DT_U32 = 8, CX_DT_F32 = 9, CX_DT_I64 = 10, CX_DT_U64 = 11, CX_DT_F64 = 12
+};
+#define CX_MAX_RANK 8
+typedef struct cx_checkpoint cx_checkpoint;
+int cx_checkpoint_open(const char* path, cx_checkpoint** ck);
+void cx_checkpoint_close(cx_checkpoint* ck);
+/* Tensor names in sorted order: i in [0, cx_checkpoint_count). */
+int32_t cx_checkpoint_count(const cx_checkpoint* ck);
+const char* cx_checkpoint_name(const cx_checkpoint* ck, int32_t i);
+/* dtype (CX_DT_*), rank, shape (CX_MAX_RANK entries), host pointer to the mapped bytes;
+ * any output may be NULL. */
+int cx_checkpoint_tensor(const cx_checkpoint* ck, const char* name, int32_t* dtype, int32_t* rank, int64_t* shape,
+                         const void** data, uint64_t* bytes);
+/* Validates the EXL3 linear `prefix` (docs/EXL3_FORMAT.md §2: prefix.trellis I16
+ * [I/16][O/16][16 K], prefix.suh F16 [I], prefix.svh F16 [O], marker prefix.mul1 =
+ * 0x83DCD12D or prefix.mcg = 0xCBAC1FED as I32 scalars, neither = 3inst; I, O multiples of
+ * 128) and returns its geometry.  The loader check of engine/model/flashnext/model.h:503-512. */
+int cx_exl3_linear_info(const cx_checkpoint* ck, const char* prefix, int32_t* in_features, int32_t* out_features,
+                        int32_t* k2, int32_t* codebook);
+/* Uploads the linear into caller-owned device buffers (tiles: cx_exl3_tile_bytes; suh,
+ * svh: I and O halves; staging: at least the trellis bytes, I O K / 8) and repacks it on
+ * the device; *m describes the result.  Returns after the uploads finished.  Replaces the
+ * repack-on-load of engine/model/flashnext/model.h:513-527. */
+int cx_exl3_load_linear(const cx_checkpoint* ck, const char* prefix, cx_exl3_matrix* m, uint32_t* tiles,
+                        uint16_t* suh, uint16_t* svh, void* staging, size_t staging_bytes, cx_stream_t stream);
+/* The reason for the calling thread's last CX_E_FORMAT (or other checkpoint) error. */
+const char* cx_last_error(void);
 
 /* Library version string. */
 const char* cx_version(void);
