@@ -1,5 +1,7 @@
 // EXL3 linear op on MI355X: loader repack, bit-exact dequant, and the linear
 // (input transform -> fused decode/MFMA GEMM -> fixed-order split sum + output transform).
+#include <vector>
+
 #include "internal.hpp"
 
 namespace cx {
@@ -55,57 +57,67 @@ __global__ void __launch_bounds__(256) DequantKernel(const uint32_t* __restrict_
 
 // ---- activation transforms ----------------------------------------------------------
 
-// Input transform of fp16 rows: RoundH(x * suh) -> WHT128 -> * norm -> fp16, stored in
-// MFMA row order.  One 128-block per 16 lanes.  ref/exl3_ref.py:140-152;
-// engine/exl3/exl3.h:48-65.
-__global__ void __launch_bounds__(256) InputTransformKernel(const __half* __restrict__ x, int ldx,
-                                                            const __half* __restrict__ suh, __half* __restrict__ xp,
-                                                            int M, int I) {
-  const int nb = I / 128;
+// Input transforms of a group of linears over the same M rows: RoundH(RoundH(x) * suh)
+// -> WHT128 -> * norm -> fp16, stored in MFMA row order.  One 128-block per 16 lanes; job
+// j owns the 16-lane items [item0, item0 + M I / 128).  ref/exl3_ref.py:140-152;
+// engine/exl3/exl3.h:48-65 (fp32 sources are rounded to fp16 first, as LinInLane does).
+__global__ void __launch_bounds__(256) InputTransformKernel(XfInTable t) {
   const int item = (blockIdx.x * blockDim.x + threadIdx.x) >> 4;
-  if (item >= M * nb) return;
-  const int r = item / nb, blk = item % nb, j = threadIdx.x & 15;
+  int jb = 0;
+  while (jb + 1 < t.n && item >= t.job[jb + 1].item0) ++jb;
+  const XfIn& J = t.job[jb];
+  const int nb = J.I / 128, local = item - J.item0;
+  if (local >= t.M * nb) return;  // whole 16-lane groups
+  const int r = local / nb, blk = local % nb, j = threadIdx.x & 15;
   const int c0 = blk * 128 + 8 * j;
   float v[8], s[8];
-  LoadH8(x + (size_t)r * ldx + c0, v);
-  LoadH8(suh + c0, s);
+  if (J.xf32) {
+    LoadF8(static_cast<const float*>(J.x) + (size_t)r * J.ldx + c0, v);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = RoundH(v[i]);
+  } else {
+    LoadH8(static_cast<const __half*>(J.x) + (size_t)r * J.ldx + c0, v);
+  }
+  LoadH8(J.suh + c0, s);
 #pragma unroll
   for (int i = 0; i < 8; ++i) v[i] = RoundH(v[i] * s[i]);
   Wht128x8(v);
-  StorePerm32x8(xp + (size_t)r * I + blk * 128, v, kHadNorm);
+  StorePerm32x8(J.xp + (size_t)r * J.I + blk * 128, v, kHadNorm);
 }
 
-// Fixed-order sum of S K-segment partials, then the output transform.
-// f16 = 0: WHT in fp32, * (norm * svh) (engine LinOutBlock, engine/exl3/exl3.h:69-82).
-// f16 = 1: y_h rounded to fp16, WHT, * norm -> fp16, * svh -> fp16 (ref/exl3_ref.py:153-156).
-__global__ void __launch_bounds__(256) OutputTransformKernel(const float* __restrict__ part, long long seg_stride,
-                                                             int S, const __half* __restrict__ svh, void* y, int M,
-                                                             int O, int f16) {
-  const int nb = O / 128;
+// Fixed-order sum of S K-segment partials, then the output transform, for a group of
+// linears.  f16 = 0: WHT in fp32, * (norm * svh) (engine LinOutBlock,
+// engine/exl3/exl3.h:69-82).  f16 = 1: y_h rounded to fp16, WHT, * norm -> fp16, * svh
+// -> fp16 (ref/exl3_ref.py:153-156).
+__global__ void __launch_bounds__(256) OutputTransformKernel(XfOutTable t) {
   const int item = (blockIdx.x * blockDim.x + threadIdx.x) >> 4;
-  if (item >= M * nb) return;
-  const int r = item / nb, blk = item % nb, j = threadIdx.x & 15;
+  int jb = 0;
+  while (jb + 1 < t.n && item >= t.job[jb + 1].item0) ++jb;
+  const XfOut& J = t.job[jb];
+  const int nb = J.O / 128, local = item - J.item0;
+  if (local >= t.M * nb) return;
+  const int r = local / nb, blk = local % nb, j = threadIdx.x & 15;
   const int c0 = blk * 128 + 8 * j;
   float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, p[8], sv[8];
-  for (int s = 0; s < S; ++s) {
-    LoadF8(part + s * seg_stride + (size_t)r * O + c0, p);
+  for (int s = 0; s < J.S; ++s) {
+    LoadF8(J.part + s * J.seg_stride + (size_t)r * J.O + c0, p);
 #pragma unroll
     for (int i = 0; i < 8; ++i) v[i] += p[i];
   }
-  if (f16) {
+  if (J.f16) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) v[i] = RoundH(v[i]);
   }
   Wht128x8(v);
-  LoadH8(svh + c0, sv);
-  if (f16) {
-    __half* d = reinterpret_cast<__half*>(y) + (size_t)r * O + c0;
+  LoadH8(J.svh + c0, sv);
+  if (J.f16) {
+    __half* d = static_cast<__half*>(J.y) + (size_t)r * J.ldy + c0;
 #pragma unroll
     for (int i = 0; i < 8; ++i) d[i] = __float2half(RoundH(v[i] * kHadNorm) * sv[i]);
   } else {
 #pragma unroll
     for (int i = 0; i < 8; ++i) v[i] *= kHadNorm * sv[i];
-    StoreF8(reinterpret_cast<float*>(y) + (size_t)r * O + c0, v);
+    StoreF8(static_cast<float*>(J.y) + (size_t)r * J.ldy + c0, v);
   }
 }
 
@@ -149,21 +161,6 @@ LinearPlan PlanLinear(int I, int O, int M) {
   return p;
 }
 
-__global__ void FillLinearTablesKernel(int4* ent, MatPtr* mat, int first, int n_entries, int chunk, int M, MatPtr m) {
-  const int i = threadIdx.x, e = first + i;
-  if (i < n_entries) ent[i] = make_int4(0, e * chunk, min(chunk, M - e * chunk), 0);
-  if (i == 0) mat[0] = m;
-}
-
-void FillLinearTables(int4* ent, MatPtr* mat, const LinearPlan& p, int M, const cx_exl3_matrix* m, hipStream_t s) {
-  const MatPtr mp{m->tiles, reinterpret_cast<const __half*>(m->suh), reinterpret_cast<const __half*>(m->svh)};
-  // Entries beyond one block of threads loop: n_entries is at most M / 64 + 1.
-  for (int base = 0; base < p.n_entries; base += 1024) {
-    const int n = std::min(1024, p.n_entries - base);
-    hipLaunchKernelGGL(FillLinearTablesKernel, dim3(1), dim3(1024), 0, s, ent + base, mat, base, n, p.chunk, M, mp);
-  }
-}
-
 bool LaunchGemm(int k2, int cb, int nrb, int ksw, int u, dim3 grid, const GemmArgs& g, hipStream_t s) {
   (void)u;
   switch (k2) {
@@ -201,11 +198,76 @@ bool LaunchGemmPrefill(int k2, int cb, int nrbt, int cpwv, dim3 grid, const Gemm
 
 
 size_t LinearWorkspace(const LinearPlan& p, int I, int O, int M) {
-  const size_t xp = AlignUp((size_t)M * I * 2, 256);
-  const size_t part = AlignUp((size_t)p.S * M * O * 4, 256);
-  const size_t ent = AlignUp((size_t)p.n_entries * 16, 256);
-  const size_t mat = AlignUp(sizeof(MatPtr), 256);
-  return xp + part + ent + mat;
+  return AlignUp((size_t)M * I * 2, 256) + AlignUp((size_t)p.S * M * O * 4, 256);
+}
+
+// One group of linears over the same M rows: the grouped input transform, one GEMM
+// launch per job (dense row entries, no device tables), the grouped output transform.
+// Jobs are checked by the caller; ws holds each job's transformed input and partials.
+int RunGroup(const cx_exl3_job* jobs, int n, int M, char* ws, hipStream_t s) {
+  XfInTable tin{};
+  XfOutTable tout{};
+  tin.n = tout.n = n;
+  tin.M = tout.M = M;
+  int in_items = 0, out_items = 0;
+  std::vector<GemmArgs> gs(n);
+  std::vector<LinearPlan> ps(n);
+  for (int j = 0; j < n; ++j) {
+    const cx_exl3_matrix* m = &jobs[j].m;
+    const int I = m->in_features, O = m->out_features;
+    const LinearPlan p = PlanLinear(I, O, M);
+    __half* xp = reinterpret_cast<__half*>(ws);
+    ws += AlignUp((size_t)M * I * 2, 256);
+    float* part = reinterpret_cast<float*>(ws);
+    ws += AlignUp((size_t)p.S * M * O * 4, 256);
+    tin.job[j] = XfIn{jobs[j].x, reinterpret_cast<const __half*>(m->suh), xp, jobs[j].ldx, I,
+                      jobs[j].x_dtype == CX_F32 ? 1 : 0, in_items};
+    in_items += M * (I / 128);
+    tout.job[j] = XfOut{part, (long long)M * O, reinterpret_cast<const __half*>(m->svh), jobs[j].y, p.S, jobs[j].ldy, O,
+                        jobs[j].y_dtype == CX_F16 ? 1 : 0, out_items};
+    out_items += M * (O / 128);
+    GemmArgs& g = gs[j];
+    g = GemmArgs{};
+    g.plane[0] = GemmPlane{nullptr, xp, part, I, O, (long long)M * O, 0};
+    g.plane[1] = g.plane[0];
+    g.entries = nullptr;
+    g.n_entries = nullptr;
+    g.n_entries_host = p.n_entries;
+    g.A = p.A;
+    g.ncp = p.ncp;
+    g.S = p.S;
+    g.mat = MatPtr{m->tiles, reinterpret_cast<const __half*>(m->suh), reinterpret_cast<const __half*>(m->svh)};
+    g.rows = M;
+    g.chunk = p.chunk;
+    ps[j] = p;
+  }
+  hipLaunchKernelGGL(InputTransformKernel, dim3((unsigned)((in_items * 16 + 255) / 256)), dim3(256), 0, s, tin);
+  for (int j = 0; j < n; ++j) {
+    const LinearPlan& p = ps[j];
+    const dim3 grid(p.ncp / (4 / p.ksw) * p.S, p.n_entries, 1);
+    if (!LaunchGemm(jobs[j].m.k2, jobs[j].m.codebook, p.nrb, p.ksw, p.u, grid, gs[j], s)) return CX_E_UNSUPPORTED;
+  }
+  hipLaunchKernelGGL(OutputTransformKernel, dim3((unsigned)((out_items * 16 + 255) / 256)), dim3(256), 0, s, tout);
+  return LaunchStatus();
+}
+
+int CheckJob(const cx_exl3_job& j) {
+  int rc = CheckMatrix(&j.m);
+  if (rc) return rc;
+  if (!j.x || !j.y) return CX_E_ARG;
+  if ((j.x_dtype != CX_F16 && j.x_dtype != CX_F32) || (j.y_dtype != CX_F16 && j.y_dtype != CX_F32)) return CX_E_ARG;
+  // Rows are read and written in 16- / 32-byte pieces.
+  if (j.ldx < j.m.in_features || j.ldy < j.m.out_features || j.ldx % 8 || j.ldy % 8) return CX_E_SHAPE;
+  return CX_OK;
+}
+
+size_t GroupWorkspace(const cx_exl3_job* jobs, int n, int M) {
+  size_t t = 0;
+  for (int j = 0; j < n; ++j) {
+    const LinearPlan p = PlanLinear(jobs[j].m.in_features, jobs[j].m.out_features, M);
+    t += LinearWorkspace(p, jobs[j].m.in_features, jobs[j].m.out_features, M);
+  }
+  return t;
 }
 
 }  // namespace cx
@@ -261,45 +323,28 @@ int cx_exl3_linear(const cx_exl3_matrix* m, const uint16_t* x, int32_t M, const 
   if (M <= 0) return CX_E_SHAPE;
   if (y_dtype != CX_F16 && y_dtype != CX_F32) return CX_E_ARG;
   if ((rc = RowOffsetsCheck(row_offsets, n_sessions, M))) return rc;
-  const int I = m->in_features, O = m->out_features;
-  const LinearPlan p = PlanLinear(I, O, M);
-  if (workspace_bytes < LinearWorkspace(p, I, O, M)) return CX_E_WORKSPACE;
-  hipStream_t s = (hipStream_t)stream;
-  char* ws = static_cast<char*>(workspace);
-  __half* xp = reinterpret_cast<__half*>(ws);
-  ws += AlignUp((size_t)M * I * 2, 256);
-  float* part = reinterpret_cast<float*>(ws);
-  ws += AlignUp((size_t)p.S * M * O * 4, 256);
-  int4* ent = reinterpret_cast<int4*>(ws);
-  ws += AlignUp((size_t)p.n_entries * 16, 256);
-  MatPtr* mat = reinterpret_cast<MatPtr*>(ws);
+  const cx_exl3_job job{*m, x, CX_F16, m->in_features, y, y_dtype, m->out_features};
+  if (workspace_bytes < GroupWorkspace(&job, 1, M)) return CX_E_WORKSPACE;
+  return RunGroup(&job, 1, M, static_cast<char*>(workspace), (hipStream_t)stream);
+}
 
-  // Row entries and the matrix pointer go down with one tiny fill kernel each call, so
-  // the sequence holds no host-side state and no memset (graph-capturable).
-  FillLinearTables(ent, mat, p, M, m, s);
-  {
-    const int items = M * (I / 128);
-    hipLaunchKernelGGL(InputTransformKernel, dim3((items * 16 + 255) / 256), dim3(256), 0, s,
-                       reinterpret_cast<const __half*>(x), I, reinterpret_cast<const __half*>(m->suh), xp, M, I);
-  }
-  GemmArgs g{};
-  g.plane[0] = GemmPlane{mat, xp, part, I, O, (long long)M * O, 0};
-  g.plane[1] = g.plane[0];
-  g.entries = ent;
-  g.n_entries = nullptr;
-  g.n_entries_host = p.n_entries;
-  g.A = p.A;
-  g.ncp = p.ncp;
-  g.S = p.S;
-  const dim3 grid(p.ncp / (4 / p.ksw) * p.S, p.n_entries, 1);
-  if (!LaunchGemm(m->k2, m->codebook, p.nrb, p.ksw, p.u, grid, g, s)) return CX_E_UNSUPPORTED;
-  {
-    const int items = M * (O / 128);
-    hipLaunchKernelGGL(OutputTransformKernel, dim3((items * 16 + 255) / 256), dim3(256), 0, s, part,
-                       (long long)M * O, p.S, reinterpret_cast<const __half*>(m->svh), y, M, O,
-                       y_dtype == CX_F16 ? 1 : 0);
-  }
-  return LaunchStatus();
+size_t cx_exl3_group_workspace_size(const cx_exl3_job* jobs, int32_t n_jobs, int32_t M) {
+  if (!jobs || n_jobs <= 0 || n_jobs > kMaxGroupJobs || M <= 0) return 0;
+  for (int j = 0; j < n_jobs; ++j)
+    if (CheckMatrix(&jobs[j].m)) return 0;
+  return GroupWorkspace(jobs, n_jobs, M);
+}
+
+int cx_exl3_group(const cx_exl3_job* jobs, int32_t n_jobs, int32_t M, const int32_t* row_offsets, int32_t n_sessions,
+                  void* workspace, size_t workspace_bytes, cx_stream_t stream) {
+  if (!jobs || !workspace) return CX_E_ARG;
+  if (n_jobs <= 0 || n_jobs > kMaxGroupJobs || M <= 0) return CX_E_SHAPE;
+  int rc;
+  for (int j = 0; j < n_jobs; ++j)
+    if ((rc = CheckJob(jobs[j]))) return rc;
+  if ((rc = RowOffsetsCheck(row_offsets, n_sessions, M))) return rc;
+  if (workspace_bytes < GroupWorkspace(jobs, n_jobs, M)) return CX_E_WORKSPACE;
+  return RunGroup(jobs, n_jobs, M, static_cast<char*>(workspace), (hipStream_t)stream);
 }
 
 const char* cx_version(void) { return "crucible-exl3-mi355x 0.1 (gfx950)"; }

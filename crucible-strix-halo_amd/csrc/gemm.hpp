@@ -62,14 +62,28 @@ struct GemmPlane {
 
 struct GemmArgs {
   GemmPlane plane[2];
-  const int4* entries;   // {matrix, row0, nrows, unused}
+  const int4* entries;   // {matrix, row0, nrows, unused}; nullptr: dense rows (below)
   const int* n_entries;  // device-side count (nullptr: use n_entries_host)
   int n_entries_host;
   int entry_base;        // blockIdx.y + entry_base indexes entries
   int A;    // k-tiles (I / 16)
   int ncp;  // column pairs (O / 32)
   int S;    // K segments across workgroups
+  // Dense rows (entries == nullptr): entry e is rows [e chunk, min(M, (e + 1) chunk)) of
+  // the single matrix `mat` (no device-side tables).
+  MatPtr mat;
+  int rows, chunk;
 };
+
+// Row entry ei: from the device table, or the dense split of rows.
+__device__ __forceinline__ int4 EntryOf(const GemmArgs& g, int ei) {
+  if (g.entries) return g.entries[ei];
+  const int r0 = ei * g.chunk;
+  return make_int4(0, r0, min(g.chunk, g.rows - r0), 0);
+}
+__device__ __forceinline__ MatPtr MatOf(const GemmArgs& g, const GemmPlane& pl, int id) {
+  return g.entries ? pl.mats[id] : g.mat;
+}
 
 // One wave streams `steps` steps of one column pair (tiles from `tiles`, already offset
 // to the wave's first step) against NRB 16-row blocks of MFMA-ordered activations
@@ -172,7 +186,7 @@ __global__ void __launch_bounds__(256) Exl3GemmKernel(GemmArgs g) {
   const int n_entries = g.n_entries ? *g.n_entries : g.n_entries_host;
   const int ei = (int)blockIdx.y + g.entry_base;
   if (ei >= n_entries) return;
-  const int4 ent = g.entries[ei];
+  const int4 ent = EntryOf(g, ei);
   const GemmPlane& pl = g.plane[blockIdx.z];
   const int ncpg = g.ncp / CPW;
   const int cpg = blockIdx.x % ncpg, kseg = blockIdx.x / ncpg;
@@ -183,7 +197,7 @@ __global__ void __launch_bounds__(256) Exl3GemmKernel(GemmArgs g) {
   const int s0 = A2 * split / nsplit, s1 = A2 * (split + 1) / nsplit;
   const int steps = s1 - s0, a0 = 2 * s0;
   const int row0 = ent.y, nrows = ent.z;
-  const MatPtr m = pl.mats[ent.x];
+  const MatPtr m = MatOf(g, pl, ent.x);
   float4_t acc[NRB][2];
   StreamColumnPair<K2, CB, NRB, U>(m.tiles + ((size_t)cp * g.A + a0) * 2 * T, steps,
                                    pl.x + (size_t)row0 * pl.ldx + a0 * 16, nrows, pl.ldx, stage[wave], lane, acc);
@@ -296,14 +310,14 @@ __global__ void __launch_bounds__(256) Exl3GemmPrefillKernel(GemmArgs g) {
   const GridPos gp = XcdEntryMajor();
   const int ei = gp.y + g.entry_base;
   if (ei >= n_entries) return;
-  const int4 ent = g.entries[ei];
+  const int4 ent = EntryOf(g, ei);
   const GemmPlane& pl = g.plane[gp.z];
   const int cpg = gp.x;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int steps = g.A / 2;
   const int row0 = ent.y, nrows = ent.z;
   const int nrb = (nrows + 15) / 16;
-  const MatPtr m = pl.mats[ent.x];
+  const MatPtr m = MatOf(g, pl, ent.x);
   const LaneRun<K2> lr(lane);
 
   __amdgpu_buffer_rsrc_t rw[CPWV];

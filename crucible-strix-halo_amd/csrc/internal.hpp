@@ -49,6 +49,30 @@ bool DispatchK2Cb(int k2, int cb, F&& f) {
   }
 }
 
+// Kernel-argument tables of the grouped activation transforms (no device-side tables).
+constexpr int kMaxGroupJobs = 16;
+struct XfIn {
+  const void* x;
+  const __half* suh;
+  __half* xp;
+  int ldx, I, xf32, item0;
+};
+struct XfInTable {
+  XfIn job[kMaxGroupJobs];
+  int n, M;
+};
+struct XfOut {
+  const float* part;
+  long long seg_stride;
+  const __half* svh;
+  void* y;
+  int S, ldy, O, f16, item0;
+};
+struct XfOutTable {
+  XfOut job[kMaxGroupJobs];
+  int n, M;
+};
+
 struct LinearPlan {
   int A, ncp;     // k-tiles, column pairs
   int nrb;        // 16-row blocks per wave
@@ -63,7 +87,6 @@ int CheckMatrix(const cx_exl3_matrix* m);
 int RowOffsetsCheck(const int32_t* row_offsets, int32_t n_sessions, int32_t M);
 LinearPlan PlanLinear(int I, int O, int M);
 size_t LinearWorkspace(const LinearPlan& p, int I, int O, int M);
-void FillLinearTables(int4* ent, MatPtr* mat, const LinearPlan& p, int M, const cx_exl3_matrix* m, hipStream_t s);
 
 // Launches Exl3GemmKernel for a runtime (rate, codebook, rows per wave, waves per
 // column pair).  Returns false for an unsupported combination.

@@ -21,6 +21,7 @@ ERRORS = {-1: "invalid argument", -2: "invalid shape", -3: "unsupported bitrate"
 
 EXPORTED = [
     "cx_exl3_tile_bytes", "cx_exl3_repack", "cx_exl3_dequant", "cx_exl3_linear_workspace_size", "cx_exl3_linear",
+    "cx_exl3_group_workspace_size", "cx_exl3_group",
     "cx_dense_linear", "cx_moe_route", "cx_moe_group_workspace_size", "cx_moe_group", "cx_moe_plan_create", "cx_moe_plan_destroy",
     "cx_moe_layer_workspace_size", "cx_moe_layer_forward", "cx_moe_layer_forward_hc", "cx_moe_plan_set_trace",
     "cx_checkpoint_open", "cx_checkpoint_close", "cx_checkpoint_count", "cx_checkpoint_name", "cx_checkpoint_tensor",
@@ -41,6 +42,11 @@ class Matrix(ctypes.Structure):
     _fields_ = [("tiles", ctypes.c_void_p), ("suh", ctypes.c_void_p), ("svh", ctypes.c_void_p),
                 ("in_features", ctypes.c_int32), ("out_features", ctypes.c_int32), ("k2", ctypes.c_int32),
                 ("codebook", ctypes.c_int32)]
+
+
+class Job(ctypes.Structure):
+    _fields_ = [("m", Matrix), ("x", ctypes.c_void_p), ("x_dtype", ctypes.c_int32), ("ldx", ctypes.c_int32),
+                ("y", ctypes.c_void_p), ("y_dtype", ctypes.c_int32), ("ldy", ctypes.c_int32)]
 
 
 class Expert(ctypes.Structure):
@@ -69,6 +75,9 @@ def lib() -> ctypes.CDLL:
         L.cx_exl3_linear_workspace_size.argtypes = [ctypes.POINTER(Matrix), I32]
         L.cx_exl3_linear_workspace_size.restype = SZ
         L.cx_exl3_linear.argtypes = [ctypes.POINTER(Matrix), P, I32, P, I32, P, I32, P, SZ, P]
+        L.cx_exl3_group_workspace_size.argtypes = [ctypes.POINTER(Job), I32, I32]
+        L.cx_exl3_group_workspace_size.restype = SZ
+        L.cx_exl3_group.argtypes = [ctypes.POINTER(Job), I32, I32, P, I32, P, SZ, P]
         L.cx_dense_linear.argtypes = [P, I32, I32, P, I32, I32, I32, P, I32, P]
         L.cx_moe_route.argtypes = [P, I32, I32, I32, I32, P, P, P, P]
         L.cx_moe_group_workspace_size.argtypes = [I32, I32, I32]
@@ -98,7 +107,7 @@ def lib() -> ctypes.CDLL:
         L.cx_exl3_load_linear.argtypes = [P, ctypes.c_char_p, ctypes.POINTER(Matrix), P, P, P, P, SZ, P]
         L.cx_last_error.restype = ctypes.c_char_p
         L.cx_version.restype = ctypes.c_char_p
-        for fn in ("cx_exl3_repack", "cx_exl3_dequant", "cx_exl3_linear", "cx_dense_linear", "cx_moe_route", "cx_moe_group",
+        for fn in ("cx_exl3_repack", "cx_exl3_dequant", "cx_exl3_linear", "cx_exl3_group", "cx_dense_linear", "cx_moe_route", "cx_moe_group",
                    "cx_moe_plan_create", "cx_moe_layer_forward", "cx_moe_layer_forward_hc", "cx_checkpoint_open",
                    "cx_checkpoint_tensor", "cx_exl3_linear_info", "cx_exl3_load_linear"):
             getattr(L, fn).restype = ctypes.c_int

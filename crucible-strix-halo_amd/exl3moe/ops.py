@@ -73,6 +73,27 @@ class DeviceLinear:
         return y
 
 
+def linear_group(jobs, row_offsets=None, workspace=None, stream=None):
+    """Runs EXL3 linears over the same rows in one group (cx_exl3_group).  jobs: list of
+    (DeviceLinear, x [M][>= I] fp16/fp32, y [M][>= O] fp16/fp32), rows contiguous in the
+    last dimension."""
+    from . import Job
+    M = jobs[0][1].shape[0]
+    arr = (Job * len(jobs))()
+    for i, (lin, x, y) in enumerate(jobs):
+        assert x.shape[0] == M and y.shape[0] == M and x.stride(1) == 1 and y.stride(1) == 1
+        assert x.dtype in (torch.float16, torch.float32) and y.dtype in (torch.float16, torch.float32)
+        arr[i] = Job(lin.struct, ptr(x), CX_F16 if x.dtype == torch.float16 else CX_F32, x.stride(0), ptr(y),
+                     CX_F16 if y.dtype == torch.float16 else CX_F32, y.stride(0))
+    if workspace is None:
+        n = int(lib().cx_exl3_group_workspace_size(arr, len(jobs), M))
+        workspace = torch.empty(max(n, 1), dtype=torch.uint8, device=jobs[0][1].device)
+    ro = i32_host(row_offsets)
+    ns = 0 if row_offsets is None else len(row_offsets) - 1
+    check("cx_exl3_group", lib().cx_exl3_group(arr, len(jobs), M, ro, ns, ptr(workspace), workspace.numel(),
+                                               stream_ptr(stream)))
+
+
 def dense_linear(W: torch.Tensor, x: torch.Tensor, y: torch.Tensor | None = None, stream=None) -> torch.Tensor:
     """y = x @ W^T for fp16 W [O][I] and fp32 or fp16 x [M][I] (the router GEMV), fp32 y."""
     O, I = W.shape

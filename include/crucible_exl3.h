@@ -105,6 +105,27 @@ typedef struct cx_moe_expert {
   cx_exl3_matrix gate, up, down;
 } cx_moe_expert;
 
+/* A group of EXL3 linears applied to the same M rows, each with its own input and output
+ * (e.g. the attention projections or the expert matrices of one decode step): one input-
+ * transform launch for all jobs, one decode-GEMM launch per job, one output-transform
+ * launch for all jobs.  Replaces Build + RunGroup over LinJobs (engine/engine.hip:
+ * 1046-1106, 1731-1746; engine/exl3/exl3.h:20-41).  fp32 inputs are rounded to fp16
+ * before the input transform, as the reference's fp32 sources are.
+ *   x   [M][ldx] of x_dtype (CX_F16 / CX_F32), y [M][ldy] of y_dtype; ldx, ldy multiples of 8
+ *   at most 16 jobs; workspace per cx_exl3_group_workspace_size */
+typedef struct cx_exl3_job {
+  cx_exl3_matrix m;
+  const void* x;
+  int32_t x_dtype;
+  int32_t ldx;
+  void* y;
+  int32_t y_dtype;
+  int32_t ldy;
+} cx_exl3_job;
+size_t cx_exl3_group_workspace_size(const cx_exl3_job* jobs, int32_t n_jobs, int32_t M);
+int cx_exl3_group(const cx_exl3_job* jobs, int32_t n_jobs, int32_t M, const int32_t* row_offsets, int32_t n_sessions,
+                  void* workspace, size_t workspace_bytes, cx_stream_t stream);
+
 /* Dense fp16-weight linear y[r][o] = W[o] . x[r] for r < M, o < O: the MoE router
  * (W = [E + 1][H], the shared-expert gate logit as output E).  Replaces LaunchDense
  * (engine/engine.hip:1824-1870) over DenseGemvKernel (engine/layers/ops.h:30-61) and the

@@ -133,3 +133,54 @@ def test_linear_errors(ops):
     small = torch.empty(16, dtype=torch.uint8, device="cuda")
     with pytest.raises(CxError):
         lin(x, workspace=small)
+
+
+def test_linear_group(ops):
+    # Three linears of different shapes, rates and input / output dtypes over the same
+    # ragged rows in one group: each job bitwise equal to its own cx_exl3_linear call
+    # (fp32 inputs rounded to fp16 first) and within tolerance of the oracle.
+    from exl3moe import synth
+    rng = np.random.default_rng(21)
+    specs = [(2048, 512, 4, np.float16, torch.float32), (512, 1024, 3, np.float32, torch.float16),
+             (1024, 256, 6, np.float32, torch.float32)]
+    offs = [0, 3, 4, 9, 13]
+    M = offs[-1]
+    jobs, singles, refs = [], [], []
+    for I, Ot, bits, xdt, ydt in specs:
+        tr, suh, svh = synth.linear(rng, I, Ot, bits)
+        lin = ops.DeviceLinear.from_trellis(tr, suh, svh, bits)
+        xb = rng.standard_normal((M, I + 64)).astype(xdt)
+        x = torch.from_numpy(xb).cuda()[:, :I]  # strided rows
+        y = torch.full((M, Ot + 8), 3.0, dtype=ydt, device="cuda")[:, :Ot]
+        jobs.append((lin, x, y))
+        x16 = torch.from_numpy(np.ascontiguousarray(xb[:, :I]).astype(np.float16)).cuda()
+        singles.append(lin(x16, ydt, row_offsets=offs).cpu().numpy())
+        w = O.reconstruct_inner(tr, bits)
+        refs.append(O.matvec(xb[:, :I].astype(np.float16), w, suh, svh,
+                             np.float32 if ydt == torch.float32 else np.float16))
+    ops.linear_group(jobs, row_offsets=offs)
+    for (lin, x, y), single, ref in zip(jobs, singles, refs):
+        got = y.cpu().numpy()
+        np.testing.assert_array_equal(got, single)
+        assert rel_l2(got, ref) <= 1e-3
+        assert torch.all(y.as_strided((M, 8), (y.stride(0), 1), y.shape[1]) == 3.0)  # padding untouched
+
+
+def test_linear_group_errors(ops):
+    from exl3moe import Job, lib, synth
+    import ctypes
+    rng = np.random.default_rng(2)
+    tr, suh, svh = synth.linear(rng, 128, 128, 4)
+    lin = ops.DeviceLinear.from_trellis(tr, suh, svh, 4)
+    x = torch.zeros(4, 128, dtype=torch.float16, device="cuda")
+    y = torch.zeros(4, 128, device="cuda")
+    ws = torch.empty(1 << 20, dtype=torch.uint8, device="cuda")
+    jobs = (Job * 17)(*[Job(lin.struct, x.data_ptr(), 0, 128, y.data_ptr(), 1, 128)] * 17)
+    assert lib().cx_exl3_group(jobs, 17, 4, None, 0, ws.data_ptr(), ws.numel(), None) == -2  # > 16 jobs
+    jobs[0].ldx = 100
+    assert lib().cx_exl3_group(jobs, 1, 4, None, 0, ws.data_ptr(), ws.numel(), None) == -2  # ldx < I
+    jobs[0].ldx = 128
+    jobs[0].x_dtype = 9
+    assert lib().cx_exl3_group(jobs, 1, 4, None, 0, ws.data_ptr(), ws.numel(), None) == -1
+    jobs[0].x_dtype = 0
+    assert lib().cx_exl3_group(jobs, 1, 4, None, 0, ws.data_ptr(), 16, None) == -4
