@@ -215,3 +215,40 @@ def test_hc_errors(ops):
     with pytest.raises(CxError) as e:
         plan.forward_hc(x, lg, post, torch.zeros(2, 3 * 256, device="cuda"))  # ldh < 4 * hidden
     assert e.value.rc == -2
+
+
+def test_config5_long_prefill_subset(ops):
+    # 8192 tokens through a 512-expert layer with gate/up at 3 bpw and down at 5 bpw
+    # (shared expert at the same rates); oracle on 32 sampled rows (rows are independent).
+    from exl3moe import synth
+    plan = synth.device_moe_layer(5, E=512, H=2048, Ie=512, topk=10, bits_gu=3, bits_d=5)
+    rng = np.random.default_rng(55)
+    M = 8192
+    x = rng.standard_normal((M, 2048)).astype(np.float16)
+    lg = rng.standard_normal((M, 513)).astype(np.float32)
+    y, sel, wts = run_layer(plan, x, lg, 2)
+    rs, rw = O.route(lg, 512, 10)
+    np.testing.assert_array_equal(sel, rs)
+    rows = np.sort(rng.choice(M, size=32, replace=False))
+    ref = oracle_layer(plan, x[rows], rs[rows], rw[rows])
+    e = rel_l2(y[rows], ref)
+    print(f"config5 rel_l2={e:.3e} max_abs={np.abs(y[rows] - ref).max():.3e}")
+    assert e <= 1e-3
+    assert np.abs(y[rows] - ref).max() <= 2e-3 * np.abs(ref).max()
+
+
+def test_config5_output_head(ops):
+    # EXL3 6-bpw head 2048 -> 151936 on the last token of 4 sessions; the output
+    # transform works per 128-column block, so column slices are checked against the
+    # oracle on the matching trellis / svh slices.
+    from exl3moe import synth
+    rng = np.random.default_rng(56)
+    tr, suh, svh = synth.linear(rng, 2048, 151936, 6)
+    lin = ops.DeviceLinear.from_trellis(tr, suh, svh, 6)
+    x = rng.standard_normal((4, 2048)).astype(np.float16)
+    y = lin(torch.from_numpy(x).cuda(), row_offsets=[0, 1, 2, 3, 4]).cpu().numpy()
+    assert np.all(np.isfinite(y))
+    for c0 in (0, 75904, 151936 - 256):
+        ts = np.ascontiguousarray(tr[:, c0 // 16:(c0 + 256) // 16])
+        ref = O.matvec(x, O.reconstruct_inner(ts, 6), suh, svh[c0:c0 + 256], np.float32)
+        assert rel_l2(y[:, c0:c0 + 256], ref) <= 1e-3
