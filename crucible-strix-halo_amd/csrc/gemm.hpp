@@ -177,8 +177,12 @@ __device__ __forceinline__ void StreamColumnPair(const uint32_t* tiles, int step
   }
 }
 
+// One 16-row block per wave (decode) at up to 4 bpw asks for 8 waves per SIMD (64
+// registers, no spills there): the decode is VALU-bound and the extra waves hide the
+// LDS round trip of each step.
 template <int K2, int CB, int NRB, int KSW, int U>
-__global__ void __launch_bounds__(256) Exl3GemmKernel(GemmArgs g) {
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NRB == 1 && K2 <= 8 ? 8 : 1)))
+Exl3GemmKernel(GemmArgs g) {
   constexpr int CPW = 4 / KSW;
   constexpr int T = TileDwords(K2);
   constexpr int DPL = (4 * T + 63) / 64;
