@@ -254,73 +254,90 @@ struct ExpertTables {
 };
 
 // Gate and up input transforms of every compact row (each matrix has its own suh):
-// RoundH(x * suh) -> WHT128 -> * norm -> fp16 in MFMA row order, 16 lanes per block.
-// engine/layers/moe_rows.h:102-125.
+// RoundH(x * suh) -> WHT128 -> * norm -> fp16 in MFMA row order.  S waves per compact
+// row: its route and expert are looked up once per wave, then lane group g (16 lanes) of
+// part t transforms the 128-blocks 4 t + g, 4 (t + S) + g, ... of both inputs (S = 1 for
+// long calls; short calls split rows for parallelism).  engine/layers/moe_rows.h:102-125.
 __global__ void __launch_bounds__(256) MoeInputKernel(const __half* __restrict__ x, const int* __restrict__ sel,
                                                       const int* __restrict__ pairs, ExpertTables tb, int M, int topk,
-                                                      int E, int H, __half* __restrict__ xg, __half* __restrict__ xu) {
-  const int nb = H / 128;
+                                                      int E, int H, int S, __half* __restrict__ xg,
+                                                      __half* __restrict__ xu) {
   const int P = M * topk + M;
-  const int item = (blockIdx.x * blockDim.x + threadIdx.x) >> 4;
-  if (item >= P * nb * 2) return;
-  const int mat = item & 1, blk = (item >> 1) % nb, p = (item >> 1) / nb;
-  const int j = threadIdx.x & 15;
+  const int w = blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+  const int p = w / S, part = w % S;
+  if (p >= P) return;  // whole waves
   int row, e;
   if (p < M * topk) {
-    const int route = pairs[p];
+    const int route = __builtin_amdgcn_readfirstlane(pairs[p]);
     row = route / topk;
-    e = sel[route];
+    e = __builtin_amdgcn_readfirstlane(sel[route]);
   } else {
     row = p - M * topk;
     e = E;
   }
-  const __half* suh = (mat ? tb.up : tb.gate)[e].suh;
-  const int c0 = blk * 128 + 8 * j;
-  float v[8], sv[8];
-  LoadH8(x + (size_t)row * H + c0, v);
-  LoadH8(suh + c0, sv);
+  const __half* sg = tb.gate[e].suh;
+  const __half* su = tb.up[e].suh;
+  const int g = (threadIdx.x >> 4) & 3, j = threadIdx.x & 15;
+  const __half* xr = x + (size_t)row * H;
+#pragma unroll 2
+  for (int blk = 4 * part + g; blk < H / 128; blk += 4 * S) {
+    const int c0 = blk * 128 + 8 * j;
+    float v[8], s1[8], s2[8], a[8];
+    LoadH8(xr + c0, v);
+    LoadH8(sg + c0, s1);
+    LoadH8(su + c0, s2);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) v[i] = RoundH(v[i] * sv[i]);
-  Wht128x8(v);
-  StorePerm32x8((mat ? xu : xg) + (size_t)p * H + blk * 128, v, kHadNorm);
+    for (int i = 0; i < 8; ++i) {
+      a[i] = RoundH(v[i] * s1[i]);
+      v[i] = RoundH(v[i] * s2[i]);
+    }
+    Wht128x8(a);
+    Wht128x8(v);
+    StorePerm32x8(xg + (size_t)p * H + blk * 128, a, kHadNorm);
+    StorePerm32x8(xu + (size_t)p * H + blk * 128, v, kHadNorm);
+  }
 }
 
 // Mid: gate and up output transforms (fp32), RoundH(RoundH(SiLU(g) * u) * suh_down),
 // WHT128, * norm -> fp16 down input in MFMA row order.  engine/layers/moe_rows.h:543-566.
+// One wave per compact row (lookups once); lane group g transforms 128-blocks g, g + 4, ...
 __global__ void __launch_bounds__(256) MoeMidKernel(const float* __restrict__ yg, const float* __restrict__ yu,
                                                     const int* __restrict__ sel, const int* __restrict__ pairs,
                                                     ExpertTables tb, int M, int topk, int E, int I,
                                                     __half* __restrict__ xd) {
-  const int nb = I / 128;
   const int P = M * topk + M;
-  const int item = (blockIdx.x * blockDim.x + threadIdx.x) >> 4;
-  if (item >= P * nb) return;
-  const int blk = item % nb, p = item / nb;
-  const int j = threadIdx.x & 15;
-  const int e = p < M * topk ? sel[pairs[p]] : E;
-  const int c0 = blk * 128 + 8 * j;
-  float g[8], u[8], svg[8], svu[8], sud[8];
-  LoadF8(yg + (size_t)p * I + c0, g);
-  LoadF8(yu + (size_t)p * I + c0, u);
+  const int p = blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+  if (p >= P) return;  // whole waves
+  const int e = p < M * topk ? __builtin_amdgcn_readfirstlane(sel[__builtin_amdgcn_readfirstlane(pairs[p])]) : E;
+  const __half* svg_p = tb.gate[e].svh;
+  const __half* svu_p = tb.up[e].svh;
+  const __half* sud_p = tb.down[e].suh;
+  const int g = (threadIdx.x >> 4) & 3, j = threadIdx.x & 15;
+  for (int blk = g; blk < I / 128; blk += 4) {
+    const int c0 = blk * 128 + 8 * j;
+    float gv[8], uv[8], svg[8], svu[8], sud[8];
+    LoadF8(yg + (size_t)p * I + c0, gv);
+    LoadF8(yu + (size_t)p * I + c0, uv);
+    LoadH8(svg_p + c0, svg);
+    LoadH8(svu_p + c0, svu);
+    LoadH8(sud_p + c0, sud);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    g[i] = 0.f + g[i];
-    u[i] = 0.f + u[i];
-  }
-  Wht128x8(g);
-  Wht128x8(u);
-  LoadH8(tb.gate[e].svh + c0, svg);
-  LoadH8(tb.up[e].svh + c0, svu);
-  LoadH8(tb.down[e].suh + c0, sud);
-  float v[8];
+    for (int i = 0; i < 8; ++i) {
+      gv[i] = 0.f + gv[i];
+      uv[i] = 0.f + uv[i];
+    }
+    Wht128x8(gv);
+    Wht128x8(uv);
+    float v[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const float gv = g[i] * (kHadNorm * svg[i]);
-    const float uv = u[i] * (kHadNorm * svu[i]);
-    v[i] = RoundH(RoundH(SiLU(gv) * uv) * sud[i]);
+    for (int i = 0; i < 8; ++i) {
+      const float a = gv[i] * (kHadNorm * svg[i]);
+      const float b = uv[i] * (kHadNorm * svu[i]);
+      v[i] = RoundH(RoundH(SiLU(a) * b) * sud[i]);
+    }
+    Wht128x8(v);
+    StorePerm32x8(xd + (size_t)p * I + blk * 128, v, kHadNorm);
   }
-  Wht128x8(v);
-  StorePerm32x8(xd + (size_t)p * I + blk * 128, v, kHadNorm);
 }
 
 // Residual write-back of the combine (hyper-connection streams): H row r, stream s at
@@ -680,16 +697,16 @@ int MoeForward(const cx_moe_plan* pl, const uint16_t* x, const float* logits, in
   if ((rc = LaunchGroup(sel, o, tiles, sz.ntiles, s))) return rc;
   mark();
   {
-    const long items = (long)sz.P * (pl->H / 128) * 2;
-    hipLaunchKernelGGL(MoeInputKernel, dim3((unsigned)((items * 16 + 255) / 256)), dim3(256), 0, s,
-                       reinterpret_cast<const __half*>(x), sel, pairs, pl->tb, M, pl->topk, pl->E, pl->H, xg, xu);
+    // Split rows over more waves when there are few of them (decode).
+    const int S = sz.P >= 4096 ? 1 : std::max(1, std::min(4, pl->H / 512));
+    hipLaunchKernelGGL(MoeInputKernel, dim3((unsigned)(((long)sz.P * S + 3) / 4)), dim3(256), 0, s,
+                       reinterpret_cast<const __half*>(x), sel, pairs, pl->tb, M, pl->topk, pl->E, pl->H, S, xg, xu);
   }
   mark();
   if (!LaunchExpertGemm(pl, sz, true, xg, xu, yg, yu, ent, nent, s)) return CX_E_UNSUPPORTED;
   mark();
   {
-    const long items = (long)sz.P * (pl->I / 128);
-    hipLaunchKernelGGL(MoeMidKernel, dim3((unsigned)((items * 16 + 255) / 256)), dim3(256), 0, s, yg, yu, sel, pairs,
+    hipLaunchKernelGGL(MoeMidKernel, dim3((unsigned)((sz.P + 3) / 4)), dim3(256), 0, s, yg, yu, sel, pairs,
                        pl->tb, M, pl->topk, pl->E, pl->I, xd);
   }
   mark();
