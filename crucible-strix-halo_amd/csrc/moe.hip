@@ -209,8 +209,19 @@ __global__ void __launch_bounds__(1024) GroupScanKernel(int* __restrict__ tile_c
   __shared__ int s_cnt[kMaxExperts];
   const int e = threadIdx.x;
   int cnt = 0;
-  if (e < o.E)
-    for (int t = 0; t < ntiles; ++t) cnt += tile_counts[(size_t)e * ntiles + t];
+  if (e < o.E) {
+    // Independent loads issued 8 at a time (a dependent chain would wait ntiles times).
+    const int* tc = tile_counts + (size_t)e * ntiles;
+    int t = 0;
+    for (; t + 8 <= ntiles; t += 8) {
+      int v[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = tc[t + i];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) cnt += v[i];
+    }
+    for (; t < ntiles; ++t) cnt += tc[t];
+  }
   int total = 0, ctotal = 0;
   const int off = BlockExclusiveScan(cnt, s_scan, &total);
   const int nch = o.entries ? (cnt + o.chunk - 1) / o.chunk : 0;
@@ -220,9 +231,21 @@ __global__ void __launch_bounds__(1024) GroupScanKernel(int* __restrict__ tile_c
     o.counts[e] = cnt;
     o.offsets[e] = off;
     int run = off;
-    for (int t = 0; t < ntiles; ++t) {
-      const int c = tile_counts[(size_t)e * ntiles + t];
-      tile_counts[(size_t)e * ntiles + t] = run;
+    int* tc = tile_counts + (size_t)e * ntiles;
+    int t = 0;
+    for (; t + 8 <= ntiles; t += 8) {
+      int v[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = tc[t + i];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        tc[t + i] = run;
+        run += v[i];
+      }
+    }
+    for (; t < ntiles; ++t) {
+      const int c = tc[t];
+      tc[t] = run;
       run += c;
     }
     if (o.entries) WriteEntries(o, e, chb, cnt, off);
