@@ -290,23 +290,25 @@ __device__ __forceinline__ GridPos XcdEntryMajor() {
   return {sub % X, 8 * (k / subs) + (L & 7), sub / X};
 }
 
-// Prefill GEMM (register-blocked): a workgroup = 4 waves owns 4 CPWV column pairs
-// (128 CPWV columns) x up to 16 NRBT rows of one expert, full K.  Each wave decodes its
-// own CPWV column pairs (B fragments stay in registers, every tile decoded once per
+// Prefill GEMM (register-blocked): a workgroup = WPG waves owns WPG CPWV column pairs
+// (32 WPG CPWV columns) x up to 16 NRBT rows of one expert, full K.  Each wave decodes
+// its own CPWV column pairs (B fragments stay in registers, every tile decoded once per
 // workgroup) and multiplies them with all the workgroup's row blocks; the activation
-// tile of a step (16 NRBT rows x 32 inputs) is loaded once into LDS and shared by the 4
-// waves.  One barrier per step double-buffers the activation tile.
-template <int K2, int CB, int NRBT, int CPWV>
-__global__ void __launch_bounds__(256) Exl3GemmPrefillKernel(GemmArgs g) {
+// tile of a step (16 NRBT rows x 32 inputs) is loaded once into LDS and shared by the
+// waves, so more waves per workgroup read the activations fewer times.  One barrier per
+// step double-buffers the activation tile.
+template <int K2, int CB, int NRBT, int CPWV, int WPG>
+__global__ void __launch_bounds__(64 * WPG) Exl3GemmPrefillKernel(GemmArgs g) {
   constexpr int T = TileDwords(K2);
   constexpr int SD = 4 * T;
   constexpr int DPL = (SD + 63) / 64;
   constexpr int ND = WindowDwords(K2);
   constexpr int R = 16 * NRBT;          // rows per workgroup
   constexpr int XS = 40;                // halves per staged row (32 + 8 pad: conflict-free 16 B reads)
-  constexpr int XL = (R * 4 + 255) / 256;  // 16-byte activation loads per thread per step
+  constexpr int NT = 64 * WPG;             // threads
+  constexpr int XL = (R * 4 + NT - 1) / NT;  // 16-byte activation loads per thread per step
   constexpr int XBYTES = 2 * R * XS * 2, EBYTES = 64 * 132 * 4;
-  __shared__ uint32_t stage[4][CPWV][StageDwords<DPL>()];
+  __shared__ uint32_t stage[WPG][CPWV][StageDwords<DPL>()];
   // Activation tiles during the main loop; the epilogue's row staging afterwards.
   __shared__ __align__(16) char smem[XBYTES > EBYTES ? XBYTES : EBYTES];
   __half(*xs)[R][XS] = reinterpret_cast<__half(*)[R][XS]>(smem);
@@ -327,7 +329,7 @@ __global__ void __launch_bounds__(256) Exl3GemmPrefillKernel(GemmArgs g) {
   __amdgpu_buffer_rsrc_t rw[CPWV];
 #pragma unroll
   for (int c = 0; c < CPWV; ++c) {
-    const int cp = (cpg * 4 + wave) * CPWV + c;
+    const int cp = (cpg * WPG + wave) * CPWV + c;
     rw[c] = MakeRsrc(m.tiles + (size_t)cp * g.A * 2 * T, (uint32_t)steps * SD * 4);
   }
   uint32_t woff[2][ND];
@@ -342,7 +344,7 @@ __global__ void __launch_bounds__(256) Exl3GemmPrefillKernel(GemmArgs g) {
   uint32_t xoff[XL];
 #pragma unroll
   for (int i = 0; i < XL; ++i) {
-    const int row = (int)threadIdx.x / 4 + 64 * i;
+    const int row = (int)threadIdx.x / 4 + (NT / 4) * i;
     xoff[i] = (uint32_t)((row * pl.ldx + 8 * (threadIdx.x & 3)) * 2);
   }
   auto load_x = [&](u32x4_t (&xv)[XL], int s) {
@@ -352,7 +354,7 @@ __global__ void __launch_bounds__(256) Exl3GemmPrefillKernel(GemmArgs g) {
   auto store_x = [&](const u32x4_t (&xv)[XL], int buf) {
 #pragma unroll
     for (int i = 0; i < XL; ++i) {
-      const int row = (int)threadIdx.x / 4 + 64 * i;
+      const int row = (int)threadIdx.x / 4 + (NT / 4) * i;
       if (row < R) *reinterpret_cast<u32x4_t*>(&xs[buf][row][8 * (threadIdx.x & 3)]) = xv[i];
     }
   };
@@ -455,10 +457,10 @@ __global__ void __launch_bounds__(256) Exl3GemmPrefillKernel(GemmArgs g) {
     float(*eb)[132] = reinterpret_cast<float(*)[132]>(smem);
     const int j = threadIdx.x & 15;
 #pragma unroll
-    for (int blk = 0; blk < CPWV; ++blk) {
+    for (int blk = 0; blk < WPG * CPWV / 4; ++blk) {
       // Column block blk of this workgroup holds column pairs 4 blk .. 4 blk + 3 of the
       // workgroup = waves (4 blk + q) / CPWV, their pair (4 blk + q) % CPWV.
-      const int c0 = (cpg * CPWV + blk) * 128 + 8 * j;
+      const int c0 = (cpg * WPG * CPWV / 4 + blk) * 128 + 8 * j;
       float sv[8];
       LoadH8(m.svh + c0, sv);
       for (int r0 = 0; r0 < nrows; r0 += 64) {
@@ -481,7 +483,7 @@ __global__ void __launch_bounds__(256) Exl3GemmPrefillKernel(GemmArgs g) {
           }
         }
         __syncthreads();
-        for (int rr = threadIdx.x >> 4; rr < 64 && r0 + rr < nrows; rr += 16) {
+        for (int rr = threadIdx.x >> 4; rr < 64 && r0 + rr < nrows; rr += NT / 16) {
           float v[8];
 #pragma unroll
           for (int e = 0; e < 8; ++e) v[e] = 0.f + eb[rr][8 * j + e];
@@ -500,7 +502,7 @@ __global__ void __launch_bounds__(256) Exl3GemmPrefillKernel(GemmArgs g) {
     if (i >= nrb) break;
 #pragma unroll
     for (int c = 0; c < CPWV; ++c) {
-      const int cp = (cpg * 4 + wave) * CPWV + c;
+      const int cp = (cpg * WPG + wave) * CPWV + c;
       const int col = (2 * cp + ((lane & 15) >> 3)) * 16 + (lane & 7);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {

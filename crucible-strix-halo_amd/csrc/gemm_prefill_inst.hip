@@ -13,18 +13,19 @@ namespace cx {
 #define CX_CAT2(a, b) a##b
 #define CX_CAT(a, b) CX_CAT2(a, b)
 
-bool CX_CAT(LaunchGemmPrefillRate, CX_RATE)(int cb, int nrbt, int cpwv, dim3 grid, const GemmArgs& g, hipStream_t s) {
+bool CX_CAT(LaunchGemmPrefillRate, CX_RATE)(int cb, int nrbt, int wpg, dim3 grid, const GemmArgs& g, hipStream_t s) {
   constexpr int K2 = CX_RATE;
-  auto go = [&](auto cbc, auto nc, auto cc) {
-    constexpr int CB = decltype(cbc)::value, NRBT = decltype(nc)::value, CPWV = decltype(cc)::value;
-    hipLaunchKernelGGL((Exl3GemmPrefillKernel<K2, CB, NRBT, CPWV>), grid, dim3(256), 0, s, g);
+  auto go = [&](auto cbc, auto nc, auto wc) {
+    constexpr int CB = decltype(cbc)::value, NRBT = decltype(nc)::value, WPG = decltype(wc)::value;
+    hipLaunchKernelGGL((Exl3GemmPrefillKernel<K2, CB, NRBT, 1, WPG>), grid, dim3(64 * WPG), 0, s, g);
     return true;
   };
   auto shape = [&](auto cbc) {
-    if (nrbt == 4 && cpwv == 1) return go(cbc, IC<4>{}, IC<1>{});
-    if (nrbt == 8 && cpwv == 1) return go(cbc, IC<8>{}, IC<1>{});
-    if (nrbt == 4 && cpwv == 2) return go(cbc, IC<4>{}, IC<2>{});
-    if (nrbt == 8 && cpwv == 2) return go(cbc, IC<8>{}, IC<2>{});
+    if (nrbt == 4 && wpg == 4) return go(cbc, IC<4>{}, IC<4>{});
+    if (nrbt == 4 && wpg == 8) return go(cbc, IC<4>{}, IC<8>{});
+    if (nrbt == 4 && wpg == 16) return go(cbc, IC<4>{}, IC<16>{});
+    if (nrbt == 8 && wpg == 4) return go(cbc, IC<8>{}, IC<4>{});
+    if (nrbt == 8 && wpg == 8) return go(cbc, IC<8>{}, IC<8>{});
     return false;
   };
   if (cb == kCbMul1) return shape(IC<kCbMul1>{});

@@ -91,12 +91,12 @@ size_t LinearWorkspace(const LinearPlan& p, int I, int O, int M);
 // Launches Exl3GemmKernel for a runtime (rate, codebook, rows per wave, waves per
 // column pair).  Returns false for an unsupported combination.
 bool LaunchGemm(int k2, int cb, int nrb, int ksw, int u, dim3 grid, const GemmArgs& g, hipStream_t s);
-// The prefill GEMM (Exl3GemmPrefillKernel): grid (O / (128 cpwv), entries padded to 8, planes).
-bool LaunchGemmPrefill(int k2, int cb, int nrbt, int cpwv, dim3 grid, const GemmArgs& g, hipStream_t s);
+// The prefill GEMM (Exl3GemmPrefillKernel): grid (O / (32 wpg), entries padded to 8, planes).
+bool LaunchGemmPrefill(int k2, int cb, int nrbt, int wpg, dim3 grid, const GemmArgs& g, hipStream_t s);
 // Per-rate launchers (one translation unit per rate, gemm_inst.hip).
 #define CX_DECLARE_RATE(K2)                                                                          \
   bool LaunchGemmRate##K2(int cb, int nrb, int ksw, dim3 grid, const GemmArgs& g, hipStream_t s); \
-  bool LaunchGemmPrefillRate##K2(int cb, int nrbt, int cpwv, dim3 grid, const GemmArgs& g, hipStream_t s);
+  bool LaunchGemmPrefillRate##K2(int cb, int nrbt, int wpg, dim3 grid, const GemmArgs& g, hipStream_t s);
 CX_DECLARE_RATE(2)
 CX_DECLARE_RATE(3)
 CX_DECLARE_RATE(4)

@@ -428,17 +428,18 @@ struct cx_moe_plan {
 namespace cx {
 
 struct MoeSizes {
-  int M, P, n, nsh, chunk, nrb, cpwv, max_entries, ntiles;
+  int M, P, n, nsh, chunk, nrb, wpg, max_entries, ntiles;
   bool small, prefill;
   size_t off_sel, off_wts, off_counts, off_offsets, off_pairs, off_rows, off_inv, off_ent, off_nent, off_tiles;
   size_t off_xg, off_xu, off_yg, off_yu, off_xd, off_yd, total;
 };
 
-// Prefill GEMM shape: a workgroup covers 16 nrb rows x 128 cpwv columns (every row of an
-// entry shares each decoded tile).  Environment overrides: CX_PREFILL_NRB (4 | 8),
-// CX_PREFILL_CPWV (1 | 2).
+// Prefill GEMM shape: a workgroup of wpg waves covers 16 nrb rows x 32 wpg columns (every
+// row of an entry shares each decoded tile, every wave of the workgroup shares the
+// activation tiles).  Environment overrides: CX_PREFILL_NRB (4 | 8), CX_PREFILL_WPG
+// (4 | 8 | 16).
 struct PrefillShape {
-  int nrb, cpwv;
+  int nrb, wpg;
 };
 PrefillShape PrefillConfig() {
   static const PrefillShape ps = [] {
@@ -446,7 +447,9 @@ PrefillShape PrefillConfig() {
       const char* e = std::getenv(k);
       return e ? std::atoi(e) : d;
     };
-    return PrefillShape{env("CX_PREFILL_NRB", 4) == 8 ? 8 : 4, env("CX_PREFILL_CPWV", 1) == 2 ? 2 : 1};
+    const int nrb = env("CX_PREFILL_NRB", 4) == 8 ? 8 : 4;
+    const int w = env("CX_PREFILL_WPG", 4);
+    return PrefillShape{nrb, w == 16 && nrb == 4 ? 16 : w == 4 ? 4 : 8};
   }();
   return ps;
 }
@@ -460,7 +463,7 @@ MoeSizes PlanMoe(const cx_moe_plan* pl, int M, int mode) {
   s.prefill = !decode;
   const PrefillShape ps = PrefillConfig();
   s.nrb = decode ? 1 : ps.nrb;
-  s.cpwv = decode ? 1 : ps.cpwv;
+  s.wpg = decode ? 4 : ps.wpg;
   // Decode: one 16-row block per entry; prefill: every row of an entry shares each decoded tile.
   s.chunk = 16 * s.nrb;
   s.nsh = (M + s.chunk - 1) / s.chunk;
@@ -538,11 +541,11 @@ bool LaunchExpertGemm(const cx_moe_plan* pl, const MoeSizes& sz, bool gate_up, c
   const int planes = gate_up ? 2 : 1;
   const int k2r = gate_up ? pl->k2_gu : pl->k2_d, cbr = gate_up ? pl->cb_gu : pl->cb_d;
   const int k2s = gate_up ? pl->k2_sgu : pl->k2_sd, cbs = gate_up ? pl->cb_sgu : pl->cb_sd;
-  const int cpwv = g.ncp % (4 * sz.cpwv) == 0 ? sz.cpwv : 1;
-  const int cpg = sz.prefill ? g.ncp / (4 * cpwv) : g.ncp / (4 / ksw);
+  const int wpg = g.ncp % sz.wpg == 0 ? sz.wpg : 4;
+  const int cpg = sz.prefill ? g.ncp / wpg : g.ncp / (4 / ksw);
   auto launch = [&](int k2, int cb, int ny) {
     if (sz.prefill)  // entry-major XCD placement needs the entry count padded to 8
-      return LaunchGemmPrefill(k2, cb, sz.nrb, cpwv, dim3(cpg, (ny + 7) / 8 * 8, planes), g, s);
+      return LaunchGemmPrefill(k2, cb, sz.nrb, wpg, dim3(cpg, (ny + 7) / 8 * 8, planes), g, s);
     return LaunchGemm(k2, cb, sz.nrb, ksw, 4, dim3(cpg, ny, planes), g, s);
   };
   if (k2r == k2s && cbr == cbs) {
