@@ -201,8 +201,34 @@ def bench_linear(seed, copies=128, warmup=10):
     t.mark()
     ms = np.array(t.ms()).reshape(copies, 2)
     t.close()
+    # The same calls captured in one HIP graph (the library records only kernel launches):
+    # the device time without the per-call host launch cost of the eager loop above.
+    graph_ms = None
+    try:
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            for i in range(copies):
+                call(warmup + i, 0)
+                call(warmup + i, 1)
+        gr.replay()
+        torch.cuda.synchronize()
+        tg = EventTimer(3, torch.cuda.current_stream().cuda_stream)
+        for _ in range(3):
+            tg.mark()
+            gr.replay()
+        tg.mark()
+        graph_ms = float(np.min(tg.ms()))
+        tg.close()
+        del gr
+    except RuntimeError as e:  # capture unsupported: report eager numbers only
+        print(f"bench.py: graph capture of the linear calls failed: {e}", file=sys.stderr)
     out = {"workload": "config2: ragged decode GEMV, 8 sessions x (1 + U{0..4}) rows, EXL3 4.0 bpw, "
                        f"rotating over {copies} seeded weight pairs", "copies": copies}
+    if graph_ms is not None:
+        Ms = np.array([batches[(warmup + i) % len(batches)][0][-1] for i in range(copies)])
+        by = sum(float((matrix_bytes(I, O, 8) + Ms * I * 2 + Ms * O * 4).sum()) for I, O in ((2048, 4096), (4096, 2048)))
+        out["graph"] = {"us_per_call": round(graph_ms * 1000 / (2 * copies), 2),
+                        "algorithmic_GBps": round(by / (graph_ms / 1000) / 1e9, 1)}
     for j, (I, O) in enumerate(((2048, 4096), (4096, 2048))):
         Ms = np.array([batches[(warmup + i) % len(batches)][0][-1] for i in range(copies)])
         by = matrix_bytes(I, O, 8) + Ms * I * 2 + Ms * O * 4
