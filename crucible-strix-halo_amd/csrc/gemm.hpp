@@ -307,7 +307,10 @@ __global__ void __launch_bounds__(64 * WPG) Exl3GemmPrefillKernel(GemmArgs g) {
   constexpr int XS = 40;                // halves per staged row (32 + 8 pad: conflict-free 16 B reads)
   constexpr int NT = 64 * WPG;             // threads
   constexpr int XL = (R * 4 + NT - 1) / NT;  // 16-byte activation loads per thread per step
-  constexpr int XBYTES = 2 * R * XS * 2, EBYTES = 64 * 132 * 4;
+  // The epilogue stages 16-row slabs (8.4 KB), so the activation tiles set the LDS size and
+  // more workgroups fit a CU.
+  constexpr int ER = 16;
+  constexpr int XBYTES = 2 * R * XS * 2, EBYTES = ER * 132 * 4;
   __shared__ uint32_t stage[WPG][CPWV][StageDwords<DPL>()];
   // Activation tiles during the main loop; the epilogue's row staging afterwards.
   __shared__ __align__(16) char smem[XBYTES > EBYTES ? XBYTES : EBYTES];
@@ -452,8 +455,8 @@ __global__ void __launch_bounds__(64 * WPG) Exl3GemmPrefillKernel(GemmArgs g) {
   }
 
   if (pl.epi == 1) {
-    // Output transform per 128-column block: stage y_h rows in LDS (reusing the
-    // activation tile area), WHT128 * norm * svh per row.
+    // Output transform per 128-column block: stage y_h rows in LDS, ER rows at a time
+    // (reusing the activation tile area), WHT128 * norm * svh per row.
     float(*eb)[132] = reinterpret_cast<float(*)[132]>(smem);
     const int j = threadIdx.x & 15;
 #pragma unroll
@@ -463,7 +466,7 @@ __global__ void __launch_bounds__(64 * WPG) Exl3GemmPrefillKernel(GemmArgs g) {
       const int c0 = (cpg * WPG * CPWV / 4 + blk) * 128 + 8 * j;
       float sv[8];
       LoadH8(m.svh + c0, sv);
-      for (int r0 = 0; r0 < nrows; r0 += 64) {
+      for (int r0 = 0; r0 < nrows; r0 += ER) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const int wpair = 4 * blk + q;  // column pair index within the workgroup
@@ -472,7 +475,7 @@ __global__ void __launch_bounds__(64 * WPG) Exl3GemmPrefillKernel(GemmArgs g) {
             const int cl = q * 32 + ((lane & 15) >> 3) * 16 + (lane & 7);
 #pragma unroll
             for (int i = 0; i < NRBT; ++i) {
-              if (i * 16 < r0 || i * 16 >= r0 + 64) continue;
+              if (i * 16 < r0 || i * 16 >= r0 + ER) continue;
 #pragma unroll
               for (int e = 0; e < 4; ++e) {
                 const int r = i * 16 - r0 + 4 * (lane >> 4) + e;
@@ -483,7 +486,7 @@ __global__ void __launch_bounds__(64 * WPG) Exl3GemmPrefillKernel(GemmArgs g) {
           }
         }
         __syncthreads();
-        for (int rr = threadIdx.x >> 4; rr < 64 && r0 + rr < nrows; rr += NT / 16) {
+        for (int rr = threadIdx.x >> 4; rr < ER && r0 + rr < nrows; rr += NT / 16) {
           float v[8];
 #pragma unroll
           for (int e = 0; e < 8; ++e) v[e] = 0.f + eb[rr][8 * j + e];
