@@ -52,6 +52,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-linear", action="store_true", help="skip the config-2 ragged linear measurement")
     ap.add_argument("--no-long", action="store_true", help="skip the config-5 long prefill + output head")
+    ap.add_argument("--no-stream", action="store_true", help="skip the device-copy HBM stream measurement")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--seed", type=int, default=2024)
     ap.add_argument("--host-data", action="store_true",
@@ -437,7 +438,8 @@ def main():
         out["linear"] = bench_linear(args.seed + 300)
     if not args.no_long:
         out["prefill_long"] = bench_long(args.seed + 400)
-    out["roofline"]["measured_stream_GBps"] = stream_peak()
+    if not args.no_stream:
+        out["roofline"]["measured_stream_GBps"] = stream_peak()
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(plans[0], batches[0], args.cpu_seconds)
     print(json.dumps(out), flush=True)
