@@ -132,16 +132,45 @@ __host__ __device__ constexpr int PermRow32(int p) {
 }
 
 // Stores 8 fp16 values of elements 8j..8j+7 of a 128-block (j = lane & 15) in the
-// 32-row MFMA order: element 8j + i goes to 32 (j >> 2) + PermPos32(8 (j & 3) + i), i.e.
-// pairs (i, i + 1) land in adjacent halves.  d: the block's first half.
+// 32-row MFMA order: element 8j + i goes to 32 (j >> 2) + PermPos32(8 (j & 3) + i), so
+// the lanes t = j & 3 of a quad hold pairs (i, i + 1) that interleave: chunk k (8 halves)
+// of the quad's 32 is [pair k of lane 0, of lane 1, of lane 2, of lane 3].  A 4 x 4
+// transpose of the packed pairs across the quad (two DPP exchange rounds) gives every
+// lane one whole chunk, stored with one 16-byte write.  d: the block's first half.
 __device__ __forceinline__ void StorePerm32x8(__half* d, const float v[8], float scale) {
-  const int j = threadIdx.x & 15;
-  const int base = 32 * (j >> 2) + 4 * ((j >> 1) & 1) + 2 * (j & 1);
+  const int j = threadIdx.x & 15, t = j & 3;
+  int h[4];
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const __half2 h = __floats2half2_rn(v[2 * k] * scale, v[2 * k + 1] * scale);
-    *reinterpret_cast<__half2*>(d + base + 8 * k) = h;
+  for (int k = 0; k < 4; ++k)
+    h[k] = __builtin_bit_cast(int, __floats2half2_rn(v[2 * k] * scale, v[2 * k + 1] * scale));
+  // Round 1 (lane ^ 1): lanes exchange the pairs whose index differs from them in bit 0.
+  {
+    const bool odd = t & 1;
+    const int a = DppI<kDppQuadSwap1>(odd ? h[0] : h[1]);
+    const int b = DppI<kDppQuadSwap1>(odd ? h[2] : h[3]);
+    if (odd) {
+      h[0] = a;
+      h[2] = b;
+    } else {
+      h[1] = a;
+      h[3] = b;
+    }
   }
+  // Round 2 (lane ^ 2): the same for bit 1.
+  {
+    const bool hi = t & 2;
+    const int a = DppI<kDppQuadSwap2>(hi ? h[0] : h[2]);
+    const int b = DppI<kDppQuadSwap2>(hi ? h[1] : h[3]);
+    if (hi) {
+      h[0] = a;
+      h[1] = b;
+    } else {
+      h[2] = a;
+      h[3] = b;
+    }
+  }
+  // Now h[q] is pair t of lane q: chunk t of the quad.
+  *reinterpret_cast<int4*>(d + 32 * (j >> 2) + 8 * t) = make_int4(h[0], h[1], h[2], h[3]);
 }
 __device__ __forceinline__ void LoadH8(const __half* p, float v[8]) {
   const uint4 u = *reinterpret_cast<const uint4*>(p);
