@@ -72,6 +72,7 @@ struct GroupOut {
   int* pairs;      // [n]  route index (row * topk + slot) in expert-major stable order
   int* row_ids;    // [n]  pairs / topk
   int* inv;        // [n]  position of route i in pairs (nullable)
+  int* expert;     // [n]  expert of compact row p (nullable)
   int4* entries;   // GEMM row entries (nullable): shared chunks first, then per-expert chunks
   int* n_entries;  // total entries
   int chunk;       // rows per entry
@@ -146,10 +147,11 @@ __device__ int StableAppend(int e, int* cursor) {
   return valid ? base + rank : -1;
 }
 
-__device__ void WritePair(const GroupOut& o, int p, int i) {
+__device__ void WritePair(const GroupOut& o, int p, int i, int e) {
   o.pairs[p] = i;
   o.row_ids[p] = i / o.topk;
   if (o.inv) o.inv[i] = p;
+  if (o.expert) o.expert[p] = e;
 }
 
 // Whole grouping in one 1024-thread workgroup (up to kSmallRoutes routes).
@@ -182,8 +184,9 @@ __global__ void __launch_bounds__(1024) GroupSmallKernel(const int* __restrict__
   __syncthreads();
   for (int base = 0; base < n; base += blockDim.x) {
     const int i = base + threadIdx.x;
-    const int p = StableAppend(i < n ? sel[i] : -1, s_cur);
-    if (p >= 0) WritePair(o, p, i);
+    const int e = i < n ? sel[i] : -1;
+    const int p = StableAppend(e, s_cur);
+    if (p >= 0) WritePair(o, p, i, e);
   }
 }
 
@@ -264,8 +267,9 @@ __global__ void __launch_bounds__(1024) GroupScatterKernel(const int* __restrict
   for (int e = threadIdx.x; e < o.E; e += blockDim.x) s_cur[e] = tile_base[(size_t)e * ntiles + blockIdx.x];
   __syncthreads();
   const int i = blockIdx.x * kTile + threadIdx.x;
-  const int p = StableAppend(i < n ? sel[i] : -1, s_cur);
-  if (p >= 0) WritePair(o, p, i);
+  const int e = i < n ? sel[i] : -1;
+  const int p = StableAppend(e, s_cur);
+  if (p >= 0) WritePair(o, p, i, e);
 }
 
 // ---- activation transforms of the experts ----------------------------------------------
@@ -281,8 +285,8 @@ struct ExpertTables {
 // row: its route and expert are looked up once per wave, then lane group g (16 lanes) of
 // part t transforms the 128-blocks 4 t + g, 4 (t + S) + g, ... of both inputs (S = 1 for
 // long calls; short calls split rows for parallelism).  engine/layers/moe_rows.h:102-125.
-__global__ void __launch_bounds__(256) MoeInputKernel(const __half* __restrict__ x, const int* __restrict__ sel,
-                                                      const int* __restrict__ pairs, ExpertTables tb, int M, int topk,
+__global__ void __launch_bounds__(256) MoeInputKernel(const __half* __restrict__ x, const int* __restrict__ rexp,
+                                                      const int* __restrict__ rows, ExpertTables tb, int M, int topk,
                                                       int E, int H, int S, __half* __restrict__ xg,
                                                       __half* __restrict__ xu) {
   const int P = M * topk + M;
@@ -290,10 +294,9 @@ __global__ void __launch_bounds__(256) MoeInputKernel(const __half* __restrict__
   const int p = w / S, part = w % S;
   if (p >= P) return;  // whole waves
   int row, e;
-  if (p < M * topk) {
-    const int route = __builtin_amdgcn_readfirstlane(pairs[p]);
-    row = route / topk;
-    e = __builtin_amdgcn_readfirstlane(sel[route]);
+  if (p < M * topk) {  // row and expert of the compact row, written by the grouping
+    row = __builtin_amdgcn_readfirstlane(rows[p]);
+    e = __builtin_amdgcn_readfirstlane(rexp[p]);
   } else {
     row = p - M * topk;
     e = E;
@@ -325,13 +328,13 @@ __global__ void __launch_bounds__(256) MoeInputKernel(const __half* __restrict__
 // WHT128, * norm -> fp16 down input in MFMA row order.  engine/layers/moe_rows.h:543-566.
 // One wave per compact row (lookups once); lane group g transforms 128-blocks g, g + 4, ...
 __global__ void __launch_bounds__(256) MoeMidKernel(const float* __restrict__ yg, const float* __restrict__ yu,
-                                                    const int* __restrict__ sel, const int* __restrict__ pairs,
+                                                    const int* __restrict__ rexp,
                                                     ExpertTables tb, int M, int topk, int E, int I,
                                                     __half* __restrict__ xd) {
   const int P = M * topk + M;
   const int p = blockIdx.x * 4 + (int)(threadIdx.x >> 6);
   if (p >= P) return;  // whole waves
-  const int e = p < M * topk ? __builtin_amdgcn_readfirstlane(sel[__builtin_amdgcn_readfirstlane(pairs[p])]) : E;
+  const int e = p < M * topk ? __builtin_amdgcn_readfirstlane(rexp[p]) : E;
   const __half* svg_p = tb.gate[e].svh;
   const __half* svu_p = tb.up[e].svh;
   const __half* sud_p = tb.down[e].suh;
@@ -430,7 +433,7 @@ namespace cx {
 struct MoeSizes {
   int M, P, n, nsh, chunk, nrb, wpg, max_entries, ntiles;
   bool small, prefill;
-  size_t off_sel, off_wts, off_counts, off_offsets, off_pairs, off_rows, off_inv, off_ent, off_nent, off_tiles;
+  size_t off_sel, off_wts, off_counts, off_offsets, off_pairs, off_rows, off_inv, off_rexp, off_ent, off_nent, off_tiles;
   size_t off_xg, off_xu, off_yg, off_yu, off_xd, off_yd, total;
 };
 
@@ -483,6 +486,7 @@ MoeSizes PlanMoe(const cx_moe_plan* pl, int M, int mode) {
   s.off_pairs = take((size_t)s.n * 4);
   s.off_rows = take((size_t)s.n * 4);
   s.off_inv = take((size_t)s.n * 4);
+  s.off_rexp = take((size_t)s.n * 4);
   s.off_ent = take((size_t)s.max_entries * 16);
   s.off_nent = take(4);
   s.off_tiles = take((size_t)pl->E * s.ntiles * 4);
@@ -601,7 +605,7 @@ int cx_moe_group(const int32_t* sel, int32_t M, int32_t E, int32_t topk, int32_t
   const int ntiles = (n + kTile - 1) / kTile;
   if (n > kSmallRoutes && (!workspace || workspace_bytes < cx_moe_group_workspace_size(M, E, topk)))
     return CX_E_WORKSPACE;
-  GroupOut o{counts, offsets, pairs, row_ids, nullptr, nullptr, nullptr, 16, M, topk, E};
+  GroupOut o{counts, offsets, pairs, row_ids, nullptr, nullptr, nullptr, nullptr, 16, M, topk, E};
   return LaunchGroup(sel, o, static_cast<int*>(workspace), ntiles, (hipStream_t)stream);
 }
 
@@ -699,6 +703,7 @@ int MoeForward(const cx_moe_plan* pl, const uint16_t* x, const float* logits, in
   int* pairs = reinterpret_cast<int*>(ws + sz.off_pairs);
   int* rows = reinterpret_cast<int*>(ws + sz.off_rows);
   int* inv = reinterpret_cast<int*>(ws + sz.off_inv);
+  int* rexp = reinterpret_cast<int*>(ws + sz.off_rexp);
   int4* ent = reinterpret_cast<int4*>(ws + sz.off_ent);
   int* nent = reinterpret_cast<int*>(ws + sz.off_nent);
   int* tiles = reinterpret_cast<int*>(ws + sz.off_tiles);
@@ -719,20 +724,20 @@ int MoeForward(const cx_moe_plan* pl, const uint16_t* x, const float* logits, in
   mark();
   LaunchRoute(logits, ld, M, pl->E, pl->topk, shared_logit, sel, wts, s);
   mark();
-  GroupOut o{counts, offsets, pairs, rows, inv, ent, nent, sz.chunk, M, pl->topk, pl->E};
+  GroupOut o{counts, offsets, pairs, rows, inv, rexp, ent, nent, sz.chunk, M, pl->topk, pl->E};
   if ((rc = LaunchGroup(sel, o, tiles, sz.ntiles, s))) return rc;
   mark();
   {
     // Split rows over more waves when there are few of them (decode).
     const int S = sz.P >= 4096 ? 1 : std::max(1, std::min(4, pl->H / 512));
     hipLaunchKernelGGL(MoeInputKernel, dim3((unsigned)(((long)sz.P * S + 3) / 4)), dim3(256), 0, s,
-                       reinterpret_cast<const __half*>(x), sel, pairs, pl->tb, M, pl->topk, pl->E, pl->H, S, xg, xu);
+                       reinterpret_cast<const __half*>(x), rexp, rows, pl->tb, M, pl->topk, pl->E, pl->H, S, xg, xu);
   }
   mark();
   if (!LaunchExpertGemm(pl, sz, true, xg, xu, yg, yu, ent, nent, s)) return CX_E_UNSUPPORTED;
   mark();
   {
-    hipLaunchKernelGGL(MoeMidKernel, dim3((unsigned)((sz.P + 3) / 4)), dim3(256), 0, s, yg, yu, sel, pairs,
+    hipLaunchKernelGGL(MoeMidKernel, dim3((unsigned)((sz.P + 3) / 4)), dim3(256), 0, s, yg, yu, rexp,
                        pl->tb, M, pl->topk, pl->E, pl->I, xd);
   }
   mark();
