@@ -141,7 +141,11 @@ __device__ __forceinline__ void StreamColumnPair(const uint32_t* tiles, int step
   };
 
   // Register double buffering: the loads of the next U steps are in flight while the
-  // current U steps are decoded; then the remaining (< U) steps one at a time.
+  // current U steps are decoded.  Loads are issued unconditionally, also past the last
+  // step: weight loads there fall outside the buffer resource (no memory access, zeros)
+  // and their results are not used.  Conditional loads would make the compiler wait for
+  // every outstanding load at each group (vmcnt(0)), since it cannot count them on every
+  // path.
   Dwords<DPL> wa[U], wb[U];
   u32x4_t xa[U][NRB], xb[U][NRB];
   auto load_group = [&](Dwords<DPL> (&w)[U], u32x4_t (&xg)[U][NRB], int sb) {
@@ -152,28 +156,16 @@ __device__ __forceinline__ void StreamColumnPair(const uint32_t* tiles, int step
       for (int rb = 0; rb < NRB; ++rb) xg[u][rb] = load_x(sb + u, rb);
     }
   };
-  int s = 0;
-  if (steps >= U) load_group(wa, xa, 0);
-  while (s + U <= steps) {
-    const bool more = s + 2 * U <= steps;
-    if (more) load_group(wb, xb, s + U);
+  load_group(wa, xa, 0);
+  for (int s = 0; s < steps; s += 2 * U) {
+    load_group(wb, xb, s + U);
 #pragma unroll
-    for (int u = 0; u < U; ++u) step(wa[u], xa[u]);
-    s += U;
-    if (!more) break;
-    const bool more2 = s + 2 * U <= steps;
-    if (more2) load_group(wa, xa, s + U);
+    for (int u = 0; u < U; ++u)
+      if (s + u < steps) step(wa[u], xa[u]);
+    load_group(wa, xa, s + 2 * U);
 #pragma unroll
-    for (int u = 0; u < U; ++u) step(wb[u], xb[u]);
-    s += U;
-    if (!more2) break;
-  }
-  for (; s < steps; ++s) {
-    const Dwords<DPL> w1 = load_w(s);
-    u32x4_t x1[NRB];
-#pragma unroll
-    for (int rb = 0; rb < NRB; ++rb) x1[rb] = load_x(s, rb);
-    step(w1, x1);
+    for (int u = 0; u < U; ++u)
+      if (s + U + u < steps) step(wb[u], xb[u]);
   }
 }
 
