@@ -364,16 +364,18 @@ __global__ void __launch_bounds__(64 * WPG) Exl3GemmPrefillKernel(GemmArgs g) {
   constexpr int PFX = 3;  // activation steps in flight
   Dwords<DPL> wq[PFW][CPWV];
   u32x4_t xq[PFX][XL];
+  // Every load is unconditional, also past the last step (weight loads there fall outside
+  // the buffer resource: no memory access; activation loads read rows' other columns):
+  // with conditional loads the compiler cannot count the loads in flight and waits for
+  // all of them (vmcnt(0)) at every use, which empties the prefetch queues.
 #pragma unroll
   for (int k = 0; k < PFW; ++k)
-    if (k < steps)
 #pragma unroll
-      for (int c = 0; c < CPWV; ++c) wq[k][c] = BufLoadN<DPL>(rw[c], loff, (uint32_t)k * SD * 4);
+    for (int c = 0; c < CPWV; ++c) wq[k][c] = BufLoadN<DPL>(rw[c], loff, (uint32_t)k * SD * 4);
 #pragma unroll
-  for (int k = 0; k < PFX; ++k)
-    if (k < steps) load_x(xq[k], k);
+  for (int k = 0; k < PFX; ++k) load_x(xq[k], k);
   store_x(xq[0], 0);
-  if (PFX < steps) load_x(xq[0], PFX);
+  load_x(xq[0], PFX);
   __syncthreads();
 
   uint32_t* slot[CPWV];
@@ -393,10 +395,8 @@ __global__ void __launch_bounds__(64 * WPG) Exl3GemmPrefillKernel(GemmArgs g) {
         if (s >= steps) break;
         const int qw = u % PFW, qx = (u + 1) % PFX;
         // Next step's activations into the other tile buffer; refill that queue slot.
-        if (s + 1 < steps) {
-          store_x(xq[qx], (s + 1) & 1);
-          if (s + 1 + PFX < steps) load_x(xq[qx], s + 1 + PFX);
-        }
+        if (s + 1 < steps) store_x(xq[qx], (s + 1) & 1);
+        load_x(xq[qx], s + 1 + PFX);
         // Decode this wave's column pairs for step s.
         half8_t b[CPWV][2];
 #pragma unroll
@@ -411,7 +411,7 @@ __global__ void __launch_bounds__(64 * WPG) Exl3GemmPrefillKernel(GemmArgs g) {
             if constexpr (ND == 2) v[j][2] = 0u;
           }
           __builtin_amdgcn_wave_barrier();
-          if (s + PFW < steps) wq[qw][c] = BufLoadN<DPL>(rw[c], loff, (uint32_t)(s + PFW) * SD * 4);
+          wq[qw][c] = BufLoadN<DPL>(rw[c], loff, (uint32_t)(s + PFW) * SD * 4);
           half4_t lo0, hi0, lo1, hi1;
           DecodeRun<K2, CB>(v[0][0], v[0][1], v[0][2], lr.shift, lo0, hi0);
           DecodeRun<K2, CB>(v[1][0], v[1][1], v[1][2], lr.shift, lo1, hi1);
