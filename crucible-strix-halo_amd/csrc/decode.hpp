@@ -149,6 +149,25 @@ struct LaneRun {
 // lo = positions 8t..8t+3, hi = 8t+4..8t+7 (fp16).
 template <int K2, int CB>
 __device__ __forceinline__ void DecodeRun(uint32_t w0, uint32_t w1, uint32_t w2, int shift, half4_t& lo, half4_t& hi) {
+  if constexpr (UniformShift(K2) && RunEnd(K2, 4) - RunEnd(K2, 0) == 16 && RunShift(K2, 0) + RunEnd(K2, 7) <= 64) {
+    // K = 4 with a lane-invariant window start: the register holding state j + 4 (low
+    // half) and state j (high half) is window bits [e - 32, e), e = end of state j + 4,
+    // i.e. one funnel shift of (w0, w1) by a compile-time amount.
+    constexpr int S0 = RunShift(K2, 0);
+    uint32_t c[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int e = S0 + RunEnd(K2, j + 4);  // bit position after the state, from w0's MSB
+      const uint32_t r = e == 64 ? w1 : AlignBit(w0, w1, (uint32_t)(64 - e));
+      c[j] = CodeTerm<CB, true>(r);
+      c[j + 4] = CodeTerm<CB, false>(r);
+    }
+    const half2_t p0 = PairWeights<CB>(c[0], c[1]), p1 = PairWeights<CB>(c[2], c[3]);
+    const half2_t p2 = PairWeights<CB>(c[4], c[5]), p3 = PairWeights<CB>(c[6], c[7]);
+    lo = half4_t{p0.x, p0.y, p1.x, p1.y};
+    hi = half4_t{p2.x, p2.y, p3.x, p3.y};
+    return;
+  }
   const uint32_t sh = UniformShift(K2) ? (uint32_t)(32 - RunShift(K2, 0)) : (uint32_t)(32 - shift);
   const uint32_t a0 = AlignBit(w0, w1, sh);
   const uint32_t a1 = AlignBit(w1, w2, sh);
