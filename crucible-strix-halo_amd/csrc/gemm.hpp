@@ -73,6 +73,10 @@ struct GemmArgs {
   // the single matrix `mat` (no device-side tables).
   MatPtr mat;
   int rows, chunk;
+  // Activation gather (nullable): compact row p < xmap_n reads activation row xmap[p]
+  // (rows at or above xmap_n read row p).  Decode GEMM only.
+  const int* xmap;
+  int xmap_n;
 };
 
 // Row entry ei: from the device table, or the dense split of rows.
@@ -88,15 +92,18 @@ __device__ __forceinline__ MatPtr MatOf(const GemmArgs& g, const GemmPlane& pl, 
 // One wave streams `steps` steps of one column pair (tiles from `tiles`, already offset
 // to the wave's first step) against NRB 16-row blocks of MFMA-ordered activations
 // (`x` at the first row, 32 k-columns per step starting at step 0) into acc.
+// `x` is the activation base at the wave's first k column; xrow[rb] is the byte offset of
+// the lane's row of block rb (at or beyond x_bytes: a row of zeros, no memory access).
 template <int K2, int CB, int NRB, int U>
-__device__ __forceinline__ void StreamColumnPair(const uint32_t* tiles, int steps, const __half* x, int nrows,
-                                                 int ldx, uint32_t* slot, int lane, float4_t (&acc)[NRB][2]) {
+__device__ __forceinline__ void StreamColumnPair(const uint32_t* tiles, int steps, const __half* x, uint32_t x_bytes,
+                                                 const uint32_t (&xrow)[NRB], uint32_t* slot, int lane,
+                                                 float4_t (&acc)[NRB][2]) {
   constexpr int T = TileDwords(K2);    // dwords per tile
   constexpr int SD = 4 * T;            // dwords per step
   constexpr int DPL = (SD + 63) / 64;  // dwords each lane loads per step
   constexpr int ND = WindowDwords(K2);
   const __amdgpu_buffer_rsrc_t rw = MakeRsrc(tiles, (uint32_t)steps * SD * 4);
-  const __amdgpu_buffer_rsrc_t rx = MakeRsrc(x, (uint32_t)nrows * ldx * 2);
+  const __amdgpu_buffer_rsrc_t rx = MakeRsrc(x, x_bytes);
   const LaneRun<K2> lr(lane);
   // LDS dword offsets of the lane's windows: run t of tile (k-tile j, column tile tau).
   uint32_t woff[2][ND];
@@ -107,7 +114,7 @@ __device__ __forceinline__ void StreamColumnPair(const uint32_t* tiles, int step
   const uint32_t loff = (uint32_t)lane * DPL * 4;
   uint32_t xoff[NRB];
 #pragma unroll
-  for (int rb = 0; rb < NRB; ++rb) xoff[rb] = (uint32_t)(((rb * 16 + (lane & 15)) * ldx + 8 * (lane >> 4)) * 2);
+  for (int rb = 0; rb < NRB; ++rb) xoff[rb] = xrow[rb] + (uint32_t)(16 * (lane >> 4));
 
 #pragma unroll
   for (int rb = 0; rb < NRB; ++rb) acc[rb][0] = acc[rb][1] = float4_t{0.f, 0.f, 0.f, 0.f};
@@ -194,9 +201,28 @@ Exl3GemmKernel(GemmArgs g) {
   const int steps = s1 - s0, a0 = 2 * s0;
   const int row0 = ent.y, nrows = ent.z;
   const MatPtr m = MatOf(g, pl, ent.x);
+  // Byte offset of each lane's activation row (rows past the entry: beyond the buffer).
+  uint32_t xrow[NRB];
+  const __half* xb;
+  uint32_t xbytes;
+  if (g.xmap) {
+#pragma unroll
+    for (int rb = 0; rb < NRB; ++rb) {
+      const int r = rb * 16 + (lane & 15), p = row0 + r;
+      const int src = p < g.xmap_n ? g.xmap[min(p, g.xmap_n - 1)] : p;
+      xrow[rb] = r < nrows ? (uint32_t)src * pl.ldx * 2 : 0xF0000000u;
+    }
+    xb = pl.x + a0 * 16;
+    xbytes = 0xE0000000u;
+  } else {
+#pragma unroll
+    for (int rb = 0; rb < NRB; ++rb) xrow[rb] = (uint32_t)((rb * 16 + (lane & 15)) * pl.ldx * 2);
+    xb = pl.x + (size_t)row0 * pl.ldx + a0 * 16;
+    xbytes = (uint32_t)nrows * pl.ldx * 2;
+  }
   float4_t acc[NRB][2];
-  StreamColumnPair<K2, CB, NRB, U>(m.tiles + ((size_t)cp * g.A + a0) * 2 * T, steps,
-                                   pl.x + (size_t)row0 * pl.ldx + a0 * 16, nrows, pl.ldx, stage[wave], lane, acc);
+  StreamColumnPair<K2, CB, NRB, U>(m.tiles + ((size_t)cp * g.A + a0) * 2 * T, steps, xb, xbytes, xrow, stage[wave],
+                                   lane, acc);
 
   if constexpr (KSW > 1) {
     // Fixed-order reduction of the K splits of each column pair.

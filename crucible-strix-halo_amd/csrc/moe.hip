@@ -20,49 +20,110 @@ constexpr int kSmallRoutes = 2048;  // single-workgroup grouping up to this many
 
 // ---- router ---------------------------------------------------------------------------
 
-// One wave per row: top-k of E logits by repeated wave argmax (logit descending, lower
-// id on ties) with DPP reductions, then the selection softmax exp(l_k - l_0) /
-// sum_j exp(l_j - l_0) summed in rank order, and sigmoid of the shared logit.
-// engine/layers/ops.h:683-713.  V = logits per lane (E <= 64 V).
+// True when (va, ia) ranks before (vb, ib): logit descending, lower expert id on ties.
+__device__ __forceinline__ bool RanksBefore(float va, int ia, float vb, int ib) {
+  return va > vb || (va == vb && ia < ib);
+}
+
+// Sorts a lane's V candidates into rank order (Batcher's odd-even merge sort, V a power
+// of two; the compare-exchanges of one stage are independent).
+template <int V>
+__device__ __forceinline__ void SortLane(float (&v)[V], int (&id)[V]) {
+#pragma unroll
+  for (int p = 1; p < V; p <<= 1)
+#pragma unroll
+    for (int k = p; k >= 1; k >>= 1)
+#pragma unroll
+      for (int j = k % p; j + k < V; j += 2 * k)
+#pragma unroll
+        for (int i = 0; i < k; ++i) {
+          const int a = i + j, b = i + j + k;
+          if (b < V && a / (2 * p) == b / (2 * p)) {
+            const bool sw = RanksBefore(v[b], id[b], v[a], id[a]);
+            const float va = v[a];
+            const int ia = id[a];
+            v[a] = sw ? v[b] : va;
+            id[a] = sw ? id[b] : ia;
+            v[b] = sw ? va : v[b];
+            id[b] = sw ? ia : id[b];
+          }
+        }
+}
+
+// Routes one row with one wave: top-k of E logits by (logit descending, id ascending),
+// then the selection softmax exp(l_k - l_0) / sum_j exp(l_j - l_0) summed in rank order,
+// and sigmoid of the shared logit.  engine/layers/ops.h:683-713.  Lane l holds logits
+// l, l + 64, ... (E <= 64 V), sorted per lane once; each of the k rounds takes the wave
+// maximum of the lane heads, and the winning lane (the only one holding the max, or the
+// lowest id among equal maxima) pops its head.  NaN logits rank as -inf.
+// Writes sel_row[0..k), wts_row[0..k] and, if s_row is given, s_row[0..k) (LDS copy).
+template <int V>
+__device__ __forceinline__ void RouteRowWave(const float* __restrict__ lg, int E, int topk, float shared,
+                                             int* __restrict__ sel_row, float* __restrict__ wts_row, int* s_row) {
+  const int lane = threadIdx.x & 63;
+  float v[V];
+  int id[V];
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    const int e = i * 64 + lane;
+    const float x = e < E ? lg[e] : -INFINITY;
+    v[i] = x == x ? x : -INFINITY;
+    id[i] = e;
+  }
+  SortLane<V>(v, id);
+  float mine = 0.f, top = 0.f;
+  int myid = 0;
+  for (int k = 0; k < topk; ++k) {
+    const float mx = WaveMaxF(v[0]);
+    const unsigned long long tie = __ballot(v[0] == mx);
+    int win;
+    if (__popcll(tie) == 1)
+      win = __builtin_amdgcn_readlane(id[0], __ffsll((long long)tie) - 1);
+    else
+      win = WaveMinI(v[0] == mx ? id[0] : 0x7fffffff);
+    if (id[0] == win) {  // ids are unique across the wave: the winning lane only
+#pragma unroll
+      for (int i = 0; i + 1 < V; ++i) {
+        v[i] = v[i + 1];
+        id[i] = id[i + 1];
+      }
+      v[V - 1] = -INFINITY;
+      id[V - 1] = 0x7fffffff;
+    }
+    if (lane == k) {
+      mine = mx;
+      myid = win;
+    }
+    if (k == 0) top = mx;
+  }
+  const float ex = lane < topk ? __expf(mine - top) : 0.f;
+  float sum = 0.f;
+  for (int k = 0; k < topk; ++k) sum += __shfl(ex, k, 64);
+  if (lane < topk) {
+    sel_row[lane] = myid;
+    wts_row[lane] = ex / sum;
+    if (s_row) s_row[lane] = myid;
+  }
+  if (lane == 0) wts_row[topk] = Sigmoid(shared);
+}
+
+// One wave per row.
 template <int V>
 __global__ void __launch_bounds__(256) RouteKernel(const float* __restrict__ logits, int ld, int M, int E, int topk,
                                                    const float* __restrict__ shared_logit, int* __restrict__ sel,
                                                    float* __restrict__ wts) {
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= M) return;  // whole waves leave together
-  const int lane = threadIdx.x & 63;
   const float* lg = logits + (size_t)row * ld;
-  float v[V];
-#pragma unroll
-  for (int i = 0; i < V; ++i) {
-    const int e = i * 64 + lane;
-    v[i] = e < E ? lg[e] : -INFINITY;
-  }
-  float mine = 0.f, top = 0.f;  // lane k < topk keeps the logit of rank k
-  unsigned taken = 0;            // bit i: this lane's logit i is selected
-  for (int k = 0; k < topk; ++k) {
-    // Lane-local best (value desc, id asc); ids of a lane increase with i.
-    float bv = -INFINITY;
-    int bi = V;
-#pragma unroll
-    for (int i = V - 1; i >= 0; --i)
-      if (v[i] >= bv && i * 64 + lane < E && !((taken >> i) & 1u)) {
-        bv = v[i];
-        bi = i;
-      }
-    const float mx = WaveMaxF(bv);
-    const int be = WaveMinI(bv == mx && bi < V ? bi * 64 + lane : 0x7fffffff);
-    if ((be & 63) == lane) taken |= 1u << (be >> 6);
-    if (lane == k) mine = mx;
-    if (k == 0) top = mx;
-    if (lane == 0) sel[(size_t)row * topk + k] = be;
-  }
-  const float ex = lane < topk ? __expf(mine - top) : 0.f;
-  float sum = 0.f;
-  for (int k = 0; k < topk; ++k) sum += __shfl(ex, k, 64);
-  if (lane < topk) wts[(size_t)row * (topk + 1) + lane] = ex / sum;
-  if (lane == 0) wts[(size_t)row * (topk + 1) + topk] = Sigmoid(shared_logit ? shared_logit[row] : lg[E]);
+  RouteRowWave<V>(lg, E, topk, shared_logit ? shared_logit[row] : lg[E], sel + (size_t)row * topk,
+                  wts + (size_t)row * (topk + 1), nullptr);
 }
+
+struct ExpertTables {
+  const MatPtr* gate;  // [E + 1], index E = shared expert
+  const MatPtr* up;
+  const MatPtr* down;
+};
 
 // ---- grouping --------------------------------------------------------------------------
 
@@ -126,8 +187,9 @@ __device__ int BlockExclusiveScan(int v, int* scratch, int* total) {
 // this wave with expert e).  Lanes of one expert are found by ballots over the id bits;
 // the waves take their cursor ranges in wave order, so positions follow route order.
 // Returns the position (or -1).  All threads of the block must call it.
-__device__ int StableAppend(int e, int* cursor) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+// nw: waves that may hold valid routes (the others have e < 0); uniform over the block.
+__device__ int StableAppend(int e, int* cursor, int nw) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const bool valid = e >= 0;
   unsigned long long peers = __ballot(valid);
 #pragma unroll
@@ -154,11 +216,9 @@ __device__ void WritePair(const GroupOut& o, int p, int i, int e) {
   if (o.expert) o.expert[p] = e;
 }
 
-// Whole grouping in one 1024-thread workgroup (up to kSmallRoutes routes).
-// ref/prefill_ref.py:37-45.
-__global__ void __launch_bounds__(1024) GroupSmallKernel(const int* __restrict__ sel, GroupOut o) {
-  __shared__ int s_cur[kMaxExperts];
-  __shared__ int s_scan[128];
+// Whole grouping in one 1024-thread workgroup (up to kSmallRoutes routes); sel may be
+// in global memory or in LDS.  ref/prefill_ref.py:37-45.
+__device__ void GroupSmallBody(const int* sel, const GroupOut& o, int* s_cur, int* s_scan) {
   const int n = o.M * o.topk;
   for (int e = threadIdx.x; e < o.E; e += blockDim.x) s_cur[e] = 0;
   __syncthreads();
@@ -166,10 +226,12 @@ __global__ void __launch_bounds__(1024) GroupSmallKernel(const int* __restrict__
   __syncthreads();
   const int e = threadIdx.x;
   const int cnt = e < o.E ? s_cur[e] : 0;
-  int total = 0, ctotal = 0;
-  const int off = BlockExclusiveScan(cnt, s_scan, &total);
   const int nch = o.entries ? (cnt + o.chunk - 1) / o.chunk : 0;
-  const int chb = BlockExclusiveScan(nch, s_scan, &ctotal);
+  // Route and chunk counts scanned together (both < 2^16 here).
+  int packed = 0;
+  const int pre = BlockExclusiveScan(cnt | (nch << 16), s_scan, &packed);
+  const int off = pre & 0xffff, chb = pre >> 16;
+  const int total = packed & 0xffff, ctotal = packed >> 16;
   if (e < o.E) {
     o.counts[e] = cnt;
     o.offsets[e] = off;
@@ -185,8 +247,59 @@ __global__ void __launch_bounds__(1024) GroupSmallKernel(const int* __restrict__
   for (int base = 0; base < n; base += blockDim.x) {
     const int i = base + threadIdx.x;
     const int e = i < n ? sel[i] : -1;
-    const int p = StableAppend(e, s_cur);
+    const int p = StableAppend(e, s_cur, min((int)blockDim.x, n - base + 63) >> 6);
     if (p >= 0) WritePair(o, p, i, e);
+  }
+}
+
+__global__ void __launch_bounds__(1024) GroupSmallKernel(const int* __restrict__ sel, GroupOut o) {
+  __shared__ int s_cur[kMaxExperts];
+  __shared__ int s_scan[128];
+  GroupSmallBody(sel, o, s_cur, s_scan);
+}
+
+// Decode: grouping and the gate/up input transforms in one launch, after routing.
+// Workgroup 0 groups all rows (GroupSmallBody); the other workgroups, a few per row, write
+// the gate and up input transforms (engine/exl3/exl3.h:48-65: RoundH(x * suh) -> WHT128 ->
+// * norm, fp16 in MFMA row order) of row r's k routed slots and of the shared expert, in
+// route order: row r * k + slot, shared expert row M k + r.  The transforms need only the
+// row's own selection, so the workgroups are independent; the gate/up GEMM gathers its
+// compact rows through pairs[].
+__global__ void __launch_bounds__(1024) GroupInputKernel(const int* __restrict__ sel, const __half* __restrict__ x,
+                                                         ExpertTables tb, int H, __half* __restrict__ xg,
+                                                         __half* __restrict__ xu, GroupOut o) {
+  __shared__ int s_e[kMaxTopK + 1];
+  __shared__ int s_cur[kMaxExperts];
+  __shared__ int s_scan[128];
+  if (blockIdx.x == 0) {
+    GroupSmallBody(sel, o, s_cur, s_scan);
+    return;
+  }
+  const int topk = o.topk, M = o.M, nb = H / 128, j = threadIdx.x & 15;
+  const int items = (topk + 1) * nb, per = blockDim.x >> 4;  // (slot, 128-block) items of a row
+  const int wpr = (items + per - 1) / per;                    // workgroups per row
+  const int row = (blockIdx.x - 1) / wpr, part = (blockIdx.x - 1) % wpr;
+  if ((int)threadIdx.x <= topk) s_e[threadIdx.x] = (int)threadIdx.x < topk ? sel[(size_t)row * topk + threadIdx.x] : o.E;
+  __syncthreads();
+  const __half* xr = x + (size_t)row * H;
+  for (int it = part * per + (threadIdx.x >> 4); it < min(items, (part + 1) * per); it += per) {
+    const int slot = it / nb, blk = it % nb;
+    const int e = s_e[slot];
+    const size_t q = slot < topk ? (size_t)row * topk + slot : (size_t)M * topk + row;
+    const int c0 = blk * 128 + 8 * j;
+    float v[8], s1[8], s2[8], a[8];
+    LoadH8(xr + c0, v);
+    LoadH8(tb.gate[e].suh + c0, s1);
+    LoadH8(tb.up[e].suh + c0, s2);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      a[i] = RoundH(v[i] * s1[i]);
+      v[i] = RoundH(v[i] * s2[i]);
+    }
+    Wht128x8(a);
+    Wht128x8(v);
+    StorePerm32x8(xg + q * H + blk * 128, a, kHadNorm);
+    StorePerm32x8(xu + q * H + blk * 128, v, kHadNorm);
   }
 }
 
@@ -268,17 +381,11 @@ __global__ void __launch_bounds__(1024) GroupScatterKernel(const int* __restrict
   __syncthreads();
   const int i = blockIdx.x * kTile + threadIdx.x;
   const int e = i < n ? sel[i] : -1;
-  const int p = StableAppend(e, s_cur);
+  const int p = StableAppend(e, s_cur, min((int)blockDim.x, n - (int)blockIdx.x * kTile + 63) >> 6);
   if (p >= 0) WritePair(o, p, i, e);
 }
 
 // ---- activation transforms of the experts ----------------------------------------------
-
-struct ExpertTables {
-  const MatPtr* gate;  // [E + 1], index E = shared expert
-  const MatPtr* up;
-  const MatPtr* down;
-};
 
 // Gate and up input transforms of every compact row (each matrix has its own suh):
 // RoundH(x * suh) -> WHT128 -> * norm -> fp16 in MFMA row order.  S waves per compact
@@ -509,6 +616,9 @@ void LaunchRoute(const float* logits, int ld, int M, int E, int topk, const floa
                        wts);
 }
 
+// Grouping fused with the input transforms (route-order rows) for small decode calls.
+bool FrontEndFits(int M, int E, int topk) { return M <= 64 && M * topk <= kSmallRoutes && E <= kMaxExperts; }
+
 int LaunchGroup(const int* sel, GroupOut& o, int* tile_counts, int ntiles, hipStream_t s) {
   const int n = o.M * o.topk;
   if (n <= kSmallRoutes) {
@@ -525,8 +635,10 @@ int LaunchGroup(const int* sel, GroupOut& o, int* tile_counts, int ntiles, hipSt
 // entries [nsh, n_entries).  Routed and shared matrices with different rates go in
 // separate launches.
 bool LaunchExpertGemm(const cx_moe_plan* pl, const MoeSizes& sz, bool gate_up, const __half* xa, const __half* xb,
-                      float* ya, float* yb, const int4* ent, const int* nent, hipStream_t s) {
+                      float* ya, float* yb, const int4* ent, const int* nent, const int* xmap, hipStream_t s) {
   GemmArgs g{};
+  g.xmap = xmap;
+  g.xmap_n = sz.n;
   const int in = gate_up ? pl->H : pl->I, out = gate_up ? pl->I : pl->H;
   g.A = in / 16;
   g.ncp = out / 32;
@@ -722,26 +834,34 @@ int MoeForward(const cx_moe_plan* pl, const uint16_t* x, const float* logits, in
     }
   };
   mark();
+  GroupOut o{counts, offsets, pairs, rows, inv, rexp, ent, nent, sz.chunk, M, pl->topk, pl->E};
+  const bool front = !sz.prefill && FrontEndFits(M, pl->E, pl->topk);
   LaunchRoute(logits, ld, M, pl->E, pl->topk, shared_logit, sel, wts, s);
   mark();
-  GroupOut o{counts, offsets, pairs, rows, inv, rexp, ent, nent, sz.chunk, M, pl->topk, pl->E};
-  if ((rc = LaunchGroup(sel, o, tiles, sz.ntiles, s))) return rc;
-  mark();
-  {
+  if (front) {
+    // Grouping and input transforms in one launch; the trace records it as the group
+    // stage (input stage empty).
+    const int wpr = ((pl->topk + 1) * (pl->H / 128) + 63) / 64;
+    hipLaunchKernelGGL(GroupInputKernel, dim3(1 + M * wpr), dim3(1024), 0, s, sel, reinterpret_cast<const __half*>(x),
+                       pl->tb, pl->H, xg, xu, o);
+    mark();
+  } else {
+    if ((rc = LaunchGroup(sel, o, tiles, sz.ntiles, s))) return rc;
+    mark();
     // Split rows over more waves when there are few of them (decode).
     const int S = sz.P >= 4096 ? 1 : std::max(1, std::min(4, pl->H / 512));
     hipLaunchKernelGGL(MoeInputKernel, dim3((unsigned)(((long)sz.P * S + 3) / 4)), dim3(256), 0, s,
                        reinterpret_cast<const __half*>(x), rexp, rows, pl->tb, M, pl->topk, pl->E, pl->H, S, xg, xu);
   }
   mark();
-  if (!LaunchExpertGemm(pl, sz, true, xg, xu, yg, yu, ent, nent, s)) return CX_E_UNSUPPORTED;
+  if (!LaunchExpertGemm(pl, sz, true, xg, xu, yg, yu, ent, nent, front ? pairs : nullptr, s)) return CX_E_UNSUPPORTED;
   mark();
   {
     hipLaunchKernelGGL(MoeMidKernel, dim3((unsigned)((sz.P + 3) / 4)), dim3(256), 0, s, yg, yu, rexp,
                        pl->tb, M, pl->topk, pl->E, pl->I, xd);
   }
   mark();
-  if (!LaunchExpertGemm(pl, sz, false, xd, nullptr, yd, nullptr, ent, nent, s)) return CX_E_UNSUPPORTED;
+  if (!LaunchExpertGemm(pl, sz, false, xd, nullptr, yd, nullptr, ent, nent, nullptr, s)) return CX_E_UNSUPPORTED;
   mark();
   {
     const long items = (long)M * (pl->H / 4);

@@ -58,6 +58,29 @@ def test_route_exact(ops):
         np.testing.assert_allclose(wts.cpu().numpy(), rw, rtol=2e-6, atol=1e-7)
 
 
+def test_route_heavy_ties(ops):
+    # Logits on a coarse grid: most rounds see several lanes holding the same maximum,
+    # so the lowest-id rule decides (standalone router and the fused decode router).
+    from exl3moe import synth
+    rng = np.random.default_rng(5)
+    for M, E, k in [(40, 512, 10), (300, 512, 10), (6, 1000, 16)]:
+        lg = (rng.integers(0, 6, size=(M, E + 1)) * 0.5).astype(np.float32)
+        lg[:, -1] = rng.standard_normal(M)
+        sel, wts = ops.route(torch.from_numpy(lg).cuda(), E, k)
+        rs, rw = O.route(lg, E, k)
+        np.testing.assert_array_equal(sel.cpu().numpy(), rs)
+        np.testing.assert_allclose(wts.cpu().numpy(), rw, rtol=2e-6, atol=1e-7)
+    plan = synth.device_moe_layer(13, E=64, H=256, Ie=128, topk=8)
+    for M in (1, 17, 64):
+        lg = (rng.integers(0, 3, size=(M, 65)) * 1.0).astype(np.float32)
+        x = rng.standard_normal((M, 256)).astype(np.float16)
+        y, sel, wts = run_layer(plan, x, lg, 1)
+        rs, rw = O.route(lg, 64, 8)
+        np.testing.assert_array_equal(sel, rs)
+        np.testing.assert_allclose(wts, rw, rtol=2e-6, atol=1e-7)
+        assert rel_l2(y, oracle_layer(plan, x, rs, rw)) <= 1e-3
+
+
 def test_route_shared_logit_array(ops):
     rng = np.random.default_rng(1)
     lg = rng.standard_normal((9, 512)).astype(np.float32)
