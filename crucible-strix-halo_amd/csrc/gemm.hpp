@@ -23,6 +23,7 @@
 
 #include "decode.hpp"
 
+
 namespace cx {
 
 // Per-wave LDS staging of one step: dword d of the step lives at d + 2 (d / 32), so the
@@ -328,7 +329,8 @@ __global__ void __launch_bounds__(64 * WPG) Exl3GemmPrefillKernel(GemmArgs g) {
   // The epilogue stages 16-row slabs (8.4 KB), so the activation tiles set the LDS size and
   // more workgroups fit a CU.
   constexpr int ER = 16;
-  constexpr int XBYTES = 2 * R * XS * 2, EBYTES = ER * 132 * 4;
+  constexpr int NXB = 4;  // activation tile buffers (written for s + 1, read by the MFMAs of s - 1)
+  constexpr int XBYTES = NXB * R * XS * 2, EBYTES = ER * 132 * 4;
   __shared__ uint32_t stage[WPG][CPWV][StageDwords<DPL>()];
   // Activation tiles during the main loop; the epilogue's row staging afterwards.
   __shared__ __align__(16) char smem[XBYTES > EBYTES ? XBYTES : EBYTES];
@@ -376,7 +378,8 @@ __global__ void __launch_bounds__(64 * WPG) Exl3GemmPrefillKernel(GemmArgs g) {
 #pragma unroll
     for (int i = 0; i < XL; ++i) {
       const int row = (int)threadIdx.x / 4 + (NT / 4) * i;
-      if (row < R) *reinterpret_cast<u32x4_t*>(&xs[buf][row][8 * (threadIdx.x & 3)]) = xv[i];
+      if ((NT / 4) * (i + 1) <= R || row < R)  // statically true when the loads cover R rows exactly
+        *reinterpret_cast<u32x4_t*>(&xs[buf][row][8 * (threadIdx.x & 3)]) = xv[i];
     }
   };
 
@@ -386,8 +389,8 @@ __global__ void __launch_bounds__(64 * WPG) Exl3GemmPrefillKernel(GemmArgs g) {
 #pragma unroll
     for (int c = 0; c < CPWV; ++c) acc[i][c][0] = acc[i][c][1] = float4_t{0.f, 0.f, 0.f, 0.f};
 
-  constexpr int PFW = 6;  // weight steps in flight
-  constexpr int PFX = 3;  // activation steps in flight
+  constexpr int PFW = 4;  // weight steps in flight
+  constexpr int PFX = 2;  // activation steps in flight
   Dwords<DPL> wq[PFW][CPWV];
   u32x4_t xq[PFX][XL];
   // Every load is unconditional, also past the last step (weight loads there fall outside
@@ -402,6 +405,10 @@ __global__ void __launch_bounds__(64 * WPG) Exl3GemmPrefillKernel(GemmArgs g) {
   for (int k = 0; k < PFX; ++k) load_x(xq[k], k);
   store_x(xq[0], 0);
   load_x(xq[0], PFX);
+  // The MFMAs issued at step 0 (for the step before the first) read tile buffer NXB - 1
+  // with zero fragments: zero it so they add exact zeros.
+  for (int i = threadIdx.x; i < R * XS / 8; i += NT)
+    reinterpret_cast<u32x4_t*>(&xs[NXB - 1][0][0])[i] = u32x4_t{0u, 0u, 0u, 0u};
   __syncthreads();
 
   uint32_t* slot[CPWV];
@@ -410,20 +417,43 @@ __global__ void __launch_bounds__(64 * WPG) Exl3GemmPrefillKernel(GemmArgs g) {
 
   // The main loop is instantiated per count of live row blocks NA, so the accumulators
   // stay in fixed registers (a runtime guard per MFMA makes the compiler copy them).
+  // Software pipeline: step s decodes its weights while the MFMAs of step s - 1 (its
+  // decoded fragments kept in registers, its activation tile still in LDS) execute, so the
+  // matrix core works under the decode's VALU stream instead of after it.
   auto main_loop = [&](auto nac) {
     constexpr int NA = decltype(nac)::value;
-    // Steps are unrolled by lcm(PFW, PFX) = 6 so every queue slot is a fixed register set.
-    constexpr int UN = 6;
+    half8_t bp[CPWV][2];  // fragments of the previous step (zero before the first)
+#pragma unroll
+    for (int c = 0; c < CPWV; ++c) bp[c][0] = bp[c][1] = half8_t{};
+    // MFMAs of row blocks [i0, i1) of the previous step.
+    auto mfma = [&](int buf, int i0, int i1) {
+#pragma unroll
+      for (int i = 0; i < NRBT; ++i) {
+        if (i < NA && i >= i0 && i < i1) {
+          const half8_t av = *reinterpret_cast<const half8_t*>(&xs[buf][i * 16 + (lane & 15)][8 * (lane >> 4)]);
+#pragma unroll
+          for (int c = 0; c < CPWV; ++c) {
+            acc[i][c][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bp[c][0], acc[i][c][0], 0, 0, 0);
+            acc[i][c][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bp[c][1], acc[i][c][1], 0, 0, 0);
+          }
+        }
+      }
+    };
+    constexpr int HALF = (NA + 1) / 2;
+    // Unrolled by lcm(PFW, PFX, NXB) = 4 (steps is a multiple of 4): every queue slot and
+    // tile buffer is fixed and a step is one basic block, so the scheduler can interleave
+    // the MFMAs of step s - 1 with the decode of step s.  Loads and tile stores past the
+    // last step are unconditional: weight loads there fall outside the buffer resource (no
+    // memory access), activation loads read rows' other columns, and the tile stored for
+    // step `steps` is never read.
+    constexpr int UN = 4;
     for (int s0 = 0; s0 < steps; s0 += UN) {
 #pragma unroll
       for (int u = 0; u < UN; ++u) {
         const int s = s0 + u;
-        if (s >= steps) break;
         const int qw = u % PFW, qx = (u + 1) % PFX;
-        // Next step's activations into the other tile buffer; refill that queue slot.
-        if (s + 1 < steps) store_x(xq[qx], (s + 1) & 1);
+        store_x(xq[qx], (u + 1) % NXB);
         load_x(xq[qx], s + 1 + PFX);
-        // Decode this wave's column pairs for step s.
         half8_t b[CPWV][2];
 #pragma unroll
         for (int c = 0; c < CPWV; ++c) {
@@ -438,27 +468,34 @@ __global__ void __launch_bounds__(64 * WPG) Exl3GemmPrefillKernel(GemmArgs g) {
           }
           __builtin_amdgcn_wave_barrier();
           wq[qw][c] = BufLoadN<DPL>(rw[c], loff, (uint32_t)(s + PFW) * SD * 4);
+          // The previous step's MFMAs go between the two runs' decode (scheduling
+          // fences keep them there): the matrix core works while the VALU decodes.
           half4_t lo0, hi0, lo1, hi1;
           DecodeRun<K2, CB>(v[0][0], v[0][1], v[0][2], lr.shift, lo0, hi0);
+          if (c == 0) {
+            __builtin_amdgcn_sched_barrier(0);
+            mfma((u + NXB - 1) % NXB, 0, HALF);
+            __builtin_amdgcn_sched_barrier(0);
+          }
           DecodeRun<K2, CB>(v[1][0], v[1][1], v[1][2], lr.shift, lo1, hi1);
+          if (c == 0) {
+            __builtin_amdgcn_sched_barrier(0);
+            mfma((u + NXB - 1) % NXB, HALF, NA);
+            __builtin_amdgcn_sched_barrier(0);
+          }
           b[c][0] = half8_t{lo0[0], lo0[1], lo0[2], lo0[3], lo1[0], lo1[1], lo1[2], lo1[3]};
           b[c][1] = half8_t{hi0[0], hi0[1], hi0[2], hi0[3], hi1[0], hi1[1], hi1[2], hi1[3]};
         }
-        const int buf = s & 1;
 #pragma unroll
-        for (int i = 0; i < NRBT; ++i) {
-          if (i < NA) {
-            const half8_t av = *reinterpret_cast<const half8_t*>(&xs[buf][i * 16 + (lane & 15)][8 * (lane >> 4)]);
-#pragma unroll
-            for (int c = 0; c < CPWV; ++c) {
-              acc[i][c][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b[c][0], acc[i][c][0], 0, 0, 0);
-              acc[i][c][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b[c][1], acc[i][c][1], 0, 0, 0);
-            }
-          }
+        for (int c = 0; c < CPWV; ++c) {
+          bp[c][0] = b[c][0];
+          bp[c][1] = b[c][1];
         }
         __syncthreads();
       }
     }
+    mfma((steps - 1) % NXB, 0, NA);
+    __syncthreads();  // the epilogue reuses the tile buffers
   };
   using std::integral_constant;
   if (nrb <= 1) main_loop(integral_constant<int, 1>{});
