@@ -80,14 +80,28 @@ struct GemmArgs {
   int xmap_n;
 };
 
+// Wave-uniform load through the scalar cache (device tables written by earlier launches).
+template <typename T>
+__device__ __forceinline__ T ScalarLoad(const T* p) {
+  static_assert(sizeof(T) % 4 == 0, "dword-sized objects only");
+  typedef const __attribute__((address_space(4))) uint32_t* ConstDwords;
+  const ConstDwords q = (ConstDwords)(p);
+  struct W {
+    uint32_t w[sizeof(T) / 4];
+  } v;
+#pragma unroll
+  for (unsigned i = 0; i < sizeof(T) / 4; ++i) v.w[i] = q[i];
+  return __builtin_bit_cast(T, v);
+}
+
 // Row entry ei: from the device table, or the dense split of rows.
 __device__ __forceinline__ int4 EntryOf(const GemmArgs& g, int ei) {
-  if (g.entries) return g.entries[ei];
+  if (g.entries) return ScalarLoad(g.entries + ei);
   const int r0 = ei * g.chunk;
   return make_int4(0, r0, min(g.chunk, g.rows - r0), 0);
 }
 __device__ __forceinline__ MatPtr MatOf(const GemmArgs& g, const GemmPlane& pl, int id) {
-  return g.entries ? pl.mats[id] : g.mat;
+  return g.entries ? ScalarLoad(pl.mats + id) : g.mat;
 }
 
 // One wave streams `steps` steps of one column pair (tiles from `tiles`, already offset
@@ -187,10 +201,12 @@ Exl3GemmKernel(GemmArgs g) {
   constexpr int T = TileDwords(K2);
   constexpr int DPL = (4 * T + 63) / 64;
   __shared__ uint32_t stage[4][StageDwords<DPL>()];
-  const int n_entries = g.n_entries ? *g.n_entries : g.n_entries_host;
+  // Device tables: entries past the last real one have 0 rows (the grid never exceeds the
+  // table), so a wave's first weight load waits on two dependent scalar loads (entry,
+  // matrix pointers) and no entry count.
   const int ei = (int)blockIdx.y + g.entry_base;
-  if (ei >= n_entries) return;
   const int4 ent = EntryOf(g, ei);
+  if (g.entries ? ent.z <= 0 : ei >= g.n_entries_host) return;
   const GemmPlane& pl = g.plane[blockIdx.z];
   const int ncpg = g.ncp / CPW;
   const int cpg = blockIdx.x % ncpg, kseg = blockIdx.x / ncpg;

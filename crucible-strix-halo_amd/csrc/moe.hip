@@ -138,7 +138,14 @@ struct GroupOut {
   int* n_entries;  // total entries
   int chunk;       // rows per entry
   int M, topk, E;
+  int max_entries;  // entries [n_entries, max_entries) are written empty (rows = 0)
 };
+
+// Empty entries after the last real one, so a GEMM launched over max_entries rows of the
+// table needs no entry count (an entry with 0 rows ends its workgroup).
+__device__ void FillEmptyEntries(const GroupOut& o, int n_real) {
+  for (int i = n_real + (int)threadIdx.x; i < o.max_entries; i += blockDim.x) o.entries[i] = make_int4(0, 0, 0, 0);
+}
 
 // Shared-expert entries [0, ceil(M / chunk)), then expert e's ceil(count / chunk) chunks,
 // in expert order.  nch_base[e]: exclusive prefix of per-expert chunk counts.
@@ -242,6 +249,7 @@ __device__ void GroupSmallBody(const int* sel, const GroupOut& o, int* s_cur, in
   if (o.entries) {
     WriteSharedEntries(o, threadIdx.x, blockDim.x);
     if (threadIdx.x == 0) *o.n_entries = (o.M + o.chunk - 1) / o.chunk + ctotal;
+    FillEmptyEntries(o, (o.M + o.chunk - 1) / o.chunk + ctotal);
   }
   __syncthreads();
   for (int base = 0; base < n; base += blockDim.x) {
@@ -370,6 +378,7 @@ __global__ void __launch_bounds__(1024) GroupScanKernel(int* __restrict__ tile_c
   if (o.entries) {
     WriteSharedEntries(o, threadIdx.x, blockDim.x);
     if (threadIdx.x == 0) *o.n_entries = (o.M + o.chunk - 1) / o.chunk + ctotal;
+    FillEmptyEntries(o, (o.M + o.chunk - 1) / o.chunk + ctotal);
   }
 }
 
@@ -834,7 +843,7 @@ int MoeForward(const cx_moe_plan* pl, const uint16_t* x, const float* logits, in
     }
   };
   mark();
-  GroupOut o{counts, offsets, pairs, rows, inv, rexp, ent, nent, sz.chunk, M, pl->topk, pl->E};
+  GroupOut o{counts, offsets, pairs, rows, inv, rexp, ent, nent, sz.chunk, M, pl->topk, pl->E, sz.max_entries};
   const bool front = !sz.prefill && FrontEndFits(M, pl->E, pl->topk);
   LaunchRoute(logits, ld, M, pl->E, pl->topk, shared_logit, sel, wts, s);
   mark();
