@@ -10,6 +10,12 @@
         counters are scaled by what they read for a plain device-to-device copy of N bytes
         in the same run (the blit kernel `__amd_rocclr_copyBuffer*`), so the result is in
         bytes whatever the counters' sampling covers.
+
+    python -m exl3moe.profile_summary counters DIR OUT.json --kernel LABEL=SUBSTR ... --cmd "..."
+        issue utilisation of the kernels whose name contains SUBSTR from one `--pmc` run with
+        GRBM_GUI_ACTIVE, SQ_ACTIVE_INST_VALU, SQ_VALU_MFMA_BUSY_CYCLES and SQ_INSTS_MFMA:
+        the fraction of SIMD cycles issuing VALU work and keeping the matrix cores busy,
+        and the MFMA issue rate in TFLOP/s against the dense fp16 peak.
 """
 from __future__ import annotations
 
@@ -91,6 +97,51 @@ def traffic(fetch_dir: str, write_dir: str, out: str, copy_bytes: int, kernel: s
     return res
 
 
+# MI355X (gfx950): 8 XCDs, 256 CUs x 4 SIMDs, 2.4 GHz peak engine clock, dense fp16 MFMA
+# peak 2.5 PFLOP/s; v_mfma_f32_16x16x32_f16 is 2 x 16 x 16 x 32 FLOP.
+XCDS, SIMDS, CLOCK_HZ, MFMA_PEAK_TFLOPS, MFMA_FLOP = 8, 1024, 2.4e9, 2500.0, 16384
+
+
+def counters(d: str, out: str, kernels: dict[str, str], cmd: str) -> dict:
+    """Per-dispatch averages of every counter of the run, and derived issue utilisation.
+
+    GRBM_GUI_ACTIVE is summed over the XCDs (one XCD's count is the kernel's duration in
+    cycles); SQ_ACTIVE_INST_VALU counts in units of 4 cycles (one wave64 VALU issue on a
+    16-lane SIMD); SQ_VALU_MFMA_BUSY_CYCLES counts SIMD cycles with the matrix core busy."""
+    tabs: dict[str, dict[str, list[float]]] = {}
+    for f in _csvs(d, "counter_collection.csv"):
+        for r in csv.DictReader(open(f)):
+            tabs.setdefault(r["Counter_Name"], {}).setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]))
+    if not tabs:
+        raise SystemExit(f"no counter rows under {d}")
+    res = {"command": cmd, "kernels": {}}
+    for label, sub in kernels.items():
+        avg = {}
+        for name, per in tabs.items():
+            vals = [v for k, vs in per.items() if sub in k for v in vs]
+            if vals:
+                avg[name] = statistics.mean(vals)
+        if "GRBM_GUI_ACTIVE" not in avg:
+            raise SystemExit(f"no dispatch of a kernel containing {sub!r} with GRBM_GUI_ACTIVE")
+        cycles = avg["GRBM_GUI_ACTIVE"] / XCDS
+        simd_cycles = cycles * SIMDS
+        k = {"substring": sub, "per_dispatch": {n: round(v, 1) for n, v in sorted(avg.items())},
+             "cycles": round(cycles), "us_at_peak_clock": round(cycles / CLOCK_HZ * 1e6, 2)}
+        if "SQ_ACTIVE_INST_VALU" in avg:
+            k["valu_busy"] = round(4 * avg["SQ_ACTIVE_INST_VALU"] / simd_cycles, 4)
+        if "SQ_VALU_MFMA_BUSY_CYCLES" in avg:
+            k["mfma_busy"] = round(avg["SQ_VALU_MFMA_BUSY_CYCLES"] / simd_cycles, 4)
+        if "SQ_INSTS_MFMA" in avg:
+            tf = avg["SQ_INSTS_MFMA"] * MFMA_FLOP / (cycles / CLOCK_HZ) / 1e12
+            k["mfma_issue_TFLOPs"] = round(tf, 1)
+            k["mfma_issue_frac_of_peak"] = round(tf / MFMA_PEAK_TFLOPS, 4)
+        res["kernels"][label] = k
+    with open(out, "w") as o:
+        json.dump(res, o, indent=1)
+        o.write("\n")
+    return res
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="what", required=True)
@@ -106,8 +157,16 @@ def main() -> None:
     t.add_argument("--copy-bytes", type=int, required=True)
     t.add_argument("--kernel", required=True)
     t.add_argument("--cmd", required=True)
+    c = sub.add_parser("counters")
+    c.add_argument("dir")
+    c.add_argument("out")
+    c.add_argument("--kernel", action="append", required=True, help="LABEL=SUBSTR")
+    c.add_argument("--cmd", required=True)
     a = ap.parse_args()
-    if a.what == "stats":
+    if a.what == "counters":
+        ks = dict(x.split("=", 1) for x in a.kernel)
+        print(json.dumps(counters(a.dir, a.out, ks, a.cmd)))
+    elif a.what == "stats":
         stats(a.dir, a.out, a.cmd, a.top)
     else:
         print(json.dumps(traffic(a.fetch_dir, a.write_dir, a.out, a.copy_bytes, a.kernel, a.cmd)))

@@ -46,3 +46,21 @@ def test_stats_table(tmp_path):
     assert lines[1] == "# command: the command"
     assert lines[3].split()[-1] == "b" and lines[4].split()[-1] == "a"
     assert lines[4].split()[1] == "2.00"
+
+
+def test_counters_utilisation(tmp_path):
+    fields = ["Kernel_Name", "Counter_Name", "Counter_Value"]
+    # One dispatch of 8 XCDs x 1000 cycles: 1024 SIMDs x 1000 SIMD-cycles.
+    rows = [{"Kernel_Name": "void cx::G<8>(a)", "Counter_Name": "GRBM_GUI_ACTIVE", "Counter_Value": 8000},
+            {"Kernel_Name": "void cx::G<8>(a)", "Counter_Name": "SQ_ACTIVE_INST_VALU", "Counter_Value": 128000},
+            {"Kernel_Name": "void cx::G<8>(a)", "Counter_Name": "SQ_VALU_MFMA_BUSY_CYCLES", "Counter_Value": 256000},
+            {"Kernel_Name": "void cx::G<8>(a)", "Counter_Name": "SQ_INSTS_MFMA", "Counter_Value": 6000},
+            {"Kernel_Name": "void cx::Other(a)", "Counter_Name": "GRBM_GUI_ACTIVE", "Counter_Value": 1}]
+    _write(tmp_path / "c" / "run_counter_collection.csv", rows, fields)
+    r = ps.counters(str(tmp_path / "c"), str(tmp_path / "c.json"), {"gemm": "G<8>"}, "cmd")
+    k = r["kernels"]["gemm"]
+    assert k["cycles"] == 1000
+    assert k["valu_busy"] == 0.5 and k["mfma_busy"] == 0.25
+    # 6000 MFMAs x 16384 FLOP in 1000 cycles at 2.4 GHz
+    assert abs(k["mfma_issue_TFLOPs"] - 6000 * 16384 / (1000 / 2.4e9) / 1e12) < 0.1
+    assert json.loads((tmp_path / "c.json").read_text())["kernels"]["gemm"]["mfma_busy"] == 0.25
