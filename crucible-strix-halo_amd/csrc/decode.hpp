@@ -57,27 +57,14 @@ __device__ __forceinline__ uint32_t AlignBit(uint32_t hi, uint32_t lo, uint32_t 
   return __builtin_amdgcn_alignbit(hi, lo, s);
 }
 
-// v_mad_u32_u16 with the 16-bit operand from the low / high half of a: a16 * b + c.
-__device__ __forceinline__ uint32_t MadU16Lo(uint32_t a, uint32_t b, uint32_t c) {
-  uint32_t d;
-  asm("v_mad_u32_u16 %0, %1, %2, %3" : "=v"(d) : "v"(a), "s"(b), "v"(c));
-  return d;
-}
-__device__ __forceinline__ uint32_t MadU16Hi(uint32_t a, uint32_t b, uint32_t c) {
-  uint32_t d;
-  asm("v_mad_u32_u16 %0, %1, %2, %3 op_sel:[1,0,0,0]" : "=v"(d) : "v"(a), "s"(b), "v"(c));
-  return d;
-}
-
-// 32-bit state * mult for the state in the low (HI = false) or high half of r: the
-// low-half product s * (mult & 0xffff) plus ((s * (mult >> 16)) mod 2^16) << 16.
+// 32-bit state * mult for the state in the low (HI = false) or high half of r: the state
+// is isolated by one shift or mask (2-cycle ops on gfx950) and multiplied by one
+// v_mul_lo_u32 (a 4-cycle op there, like the packed 16-bit multiply and v_mad_u32_u16 a
+// two-instruction 16-bit split would need).
 template <bool HI>
 __device__ __forceinline__ uint32_t StateProduct(uint32_t r, uint32_t mult) {
-  const ushort2_t v = __builtin_bit_cast(ushort2_t, r);
-  const ushort2_t s = HI ? ushort2_t{v.y, v.y} : ushort2_t{v.x, v.x};
-  const ushort2_t m = {(unsigned short)0, (unsigned short)(mult >> 16)};
-  const uint32_t t = __builtin_bit_cast(uint32_t, (ushort2_t)(s * m));
-  return HI ? MadU16Hi(r, mult & 0xffffu, t) : MadU16Lo(r, mult & 0xffffu, t);
+  const uint32_t st = HI ? (r >> 16) : (r & 0xffffu);
+  return st * mult;
 }
 
 // Per-state codebook term of the state in the low (HI = false) or high half of r.
