@@ -106,8 +106,9 @@ def counters(d: str, out: str, kernels: dict[str, str], cmd: str) -> dict:
     """Per-dispatch averages of every counter of the run, and derived issue utilisation.
 
     GRBM_GUI_ACTIVE is summed over the XCDs (one XCD's count is the kernel's duration in
-    cycles); SQ_ACTIVE_INST_VALU counts in units of 4 cycles (one wave64 VALU issue on a
-    16-lane SIMD); SQ_VALU_MFMA_BUSY_CYCLES counts SIMD cycles with the matrix core busy."""
+    cycles); SQ_ACTIVE_INST_VALU counts VALU instructions issued (taken here as 4 cycles
+    each, an upper bound); SQ_VALU_MFMA_BUSY_CYCLES counts SIMD cycles with the matrix core
+    busy."""
     tabs: dict[str, dict[str, list[float]]] = {}
     for f in _csvs(d, "counter_collection.csv"):
         for r in csv.DictReader(open(f)):
@@ -128,7 +129,11 @@ def counters(d: str, out: str, kernels: dict[str, str], cmd: str) -> dict:
         k = {"substring": sub, "per_dispatch": {n: round(v, 1) for n, v in sorted(avg.items())},
              "cycles": round(cycles), "us_at_peak_clock": round(cycles / CLOCK_HZ * 1e6, 2)}
         if "SQ_ACTIVE_INST_VALU" in avg:
-            k["valu_busy"] = round(4 * avg["SQ_ACTIVE_INST_VALU"] / simd_cycles, 4)
+            # Issue slots at 4 cycles each: an upper bound on VALU busy time (simple 32-bit
+            # ALU ops and fp32 add/FMA issue in about 2 cycles per wave64 on gfx950).
+            k["valu_busy_4cycle_slots"] = round(4 * avg["SQ_ACTIVE_INST_VALU"] / simd_cycles, 4)
+        if "SQ_INSTS_VALU" in avg:
+            k["valu_instructions_per_simd_cycle"] = round(avg["SQ_INSTS_VALU"] / simd_cycles, 4)
         if "SQ_VALU_MFMA_BUSY_CYCLES" in avg:
             k["mfma_busy"] = round(avg["SQ_VALU_MFMA_BUSY_CYCLES"] / simd_cycles, 4)
         if "SQ_INSTS_MFMA" in avg:

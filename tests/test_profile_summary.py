@@ -60,7 +60,7 @@ def test_counters_utilisation(tmp_path):
     r = ps.counters(str(tmp_path / "c"), str(tmp_path / "c.json"), {"gemm": "G<8>"}, "cmd")
     k = r["kernels"]["gemm"]
     assert k["cycles"] == 1000
-    assert k["valu_busy"] == 0.5 and k["mfma_busy"] == 0.25
+    assert k["valu_busy_4cycle_slots"] == 0.5 and k["mfma_busy"] == 0.25
     # 6000 MFMAs x 16384 FLOP in 1000 cycles at 2.4 GHz
     assert abs(k["mfma_issue_TFLOPs"] - 6000 * 16384 / (1000 / 2.4e9) / 1e12) < 0.1
     assert json.loads((tmp_path / "c.json").read_text())["kernels"]["gemm"]["mfma_busy"] == 0.25
