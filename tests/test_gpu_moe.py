@@ -162,6 +162,20 @@ def layer512(ops):
     return synth.device_moe_layer(3, E=512, H=2048, Ie=512, topk=10)
 
 
+def test_decode_rows_invariant_to_batch(ops, layer512):
+    # Decode: a row's layer output is bitwise the same whatever other rows share the call
+    # (the engine verifies draft rows against rows decoded alone).  Rows are permuted and
+    # subsets taken, so the rows' experts group differently in every call.
+    rng = np.random.default_rng(44)
+    M = 40
+    x = rng.standard_normal((M, 2048)).astype(np.float16)
+    lg = rng.standard_normal((M, 513)).astype(np.float32)
+    full, _, _ = run_layer(layer512, x, lg, 1)
+    for rows in ([0], [7, 3], list(range(5, 29)), list(rng.permutation(M)[:17])):
+        part, _, _ = run_layer(layer512, np.ascontiguousarray(x[rows]), np.ascontiguousarray(lg[rows]), 1)
+        np.testing.assert_array_equal(part.view(np.uint32), full[rows].view(np.uint32))
+
+
 def test_config3_decode(ops, layer512):
     # 8 ragged sessions of 1..5 rows, hidden fp16 N(0,1), logits fp32 N(0,1).
     from exl3moe import synth
