@@ -129,6 +129,47 @@ def run_workload(plans, batches, warmup, steps, mode):
             "M": [batches[b][0][-1] for b in order]}
 
 
+def graph_decode(plans, batches, warmup, steps, mode):
+    """The same decode steps captured in one HIP graph (the layer records only kernel
+    launches, no allocations or memsets) and replayed: the device time of the layer chain
+    without the host launch cost, as a serving loop that captures one graph per batch
+    shape sees it.  Returns ms per step (best of 3 replays) or None."""
+    import numpy as np
+    import torch
+    from exl3moe.trace import EventTimer
+    maxM = max(b[0][-1] for b in batches)
+    ws = torch.empty(max(p.workspace_size(maxM, mode) for p in plans), dtype=torch.uint8, device="cuda")
+    ys = torch.empty(maxM, H, dtype=torch.float32, device="cuda")
+    sels = [torch.empty(b[0][-1], TOPK, dtype=torch.int32, device="cuda") for b in batches]
+
+    def call(i):
+        offs, x, lg = batches[i % len(batches)]
+        plans[i % len(plans)](x, lg, row_offsets=offs, mode=mode, workspace=ws, y=ys[:offs[-1]],
+                              sel=sels[i % len(batches)])
+    try:
+        for i in range(warmup):
+            call(i)
+        torch.cuda.synchronize()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            for s in range(steps):
+                call(warmup + s)
+        gr.replay()
+        torch.cuda.synchronize()
+        tg = EventTimer(3, torch.cuda.current_stream().cuda_stream)
+        for _ in range(3):
+            tg.mark()
+            gr.replay()
+        tg.mark()
+        ms = float(np.min(tg.ms())) / steps
+        tg.close()
+        del gr
+        return ms
+    except RuntimeError as e:  # capture unsupported: report eager numbers only
+        print(f"bench.py: graph capture of the decode steps failed: {e}", file=sys.stderr)
+        return None
+
+
 def pct(v):
     import numpy as np
     v = np.asarray(v, dtype=np.float64)
@@ -415,6 +456,9 @@ def main():
                   "stage_us_mean": {n: round(float(st[:, i].mean() * 1000), 2) for i, n in enumerate(
                       ["route", "group", "input", "gate_up", "mid", "down", "combine"])}},
     }
+    gms = graph_decode(plans, batches, args.warmup, args.steps, CX_MOE_DECODE)
+    if gms is not None:
+        out["graph"] = {"tokens_per_s": round(r["rows"] / (gms * args.steps / 1000), 1), "ms_per_step": round(gms, 4)}
     if not args.no_prefill:
         pb = make_batches(2, args.seed + 200, prefill=True)
         rp = run_workload(plans, pb, 2, args.prefill_steps, CX_MOE_PREFILL)

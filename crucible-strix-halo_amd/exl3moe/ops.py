@@ -147,8 +147,13 @@ class MoePlan:
         self.handle = h
 
     def __del__(self):
-        if getattr(self, "handle", None):
-            lib().cx_moe_plan_destroy(self.handle)
+        # At interpreter exit the module globals may already be gone: the process end
+        # releases the device tables then.
+        if getattr(self, "handle", None) and lib is not None:
+            try:
+                lib().cx_moe_plan_destroy(self.handle)
+            except Exception:
+                pass
             self.handle = None
 
     def workspace_size(self, M: int, mode: int = CX_MOE_AUTO) -> int:
