@@ -22,49 +22,30 @@ __device__ __forceinline__ float H2F(__half h) { return __half2float(h); }
 __device__ __forceinline__ float SiLU(float v) { return v / (1.f + __expf(-v)); }
 __device__ __forceinline__ float Sigmoid(float v) { return 1.f / (1.f + __expf(-v)); }
 
-// 128-point natural-order Sylvester butterfly over fp32 values, 32 lanes per block
-// (a wave64 holds two blocks: lanes 0-31 and 32-63).  Lane j of a block holds elements
-// 4j..4j+3.  Strides 1 and 2 are in-lane, strides 4..64 are lane xors 1..16, in
-// increasing order, each output being lo + hi or lo - hi of the same two operands, so
-// the result is the same fp32 value as any other evaluation of that butterfly network.
-__device__ __forceinline__ void Wht128x4(float v[4]) {
-  const int lane = threadIdx.x & 31;
-  const float a0 = v[0] + v[1], a1 = v[0] - v[1], a2 = v[2] + v[3], a3 = v[2] - v[3];
-  v[0] = a0 + a2;
-  v[1] = a1 + a3;
-  v[2] = a0 - a2;
-  v[3] = a1 - a3;
-#pragma unroll
-  for (int m = 1; m < 32; m <<= 1) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float o = __shfl_xor(v[i], m, 64);
-      v[i] = (lane & m) ? (o - v[i]) : (v[i] + o);
-    }
-  }
-}
-
 // ---- cross-lane moves inside 16-lane rows (DPP, plain VALU: no LDS traffic) ----------
+// Every pattern used here reads an in-range lane of the same row with all rows and banks
+// enabled, so the moves need no `old` value (bound_ctrl set: nothing is read from it).
 template <int CTRL>
 __device__ __forceinline__ float Dpp(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xf, 0xf, true));
 }
 template <int CTRL>
 __device__ __forceinline__ int DppI(int v) {
-  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
+  return __builtin_amdgcn_mov_dpp(v, CTRL, 0xf, 0xf, true);
 }
 constexpr int kDppQuadSwap1 = 0xB1;     // quad_perm [1,0,3,2]: lane ^ 1
 constexpr int kDppQuadSwap2 = 0x4E;     // quad_perm [2,3,0,1]: lane ^ 2
 constexpr int kDppQuadReverse = 0x1B;   // quad_perm [3,2,1,0]: lane ^ 3
 constexpr int kDppRowMirror = 0x140;    // lane 15 - i within 16
 constexpr int kDppRowHalfMirror = 0x141;  // lane 7 - i within 8 (lane ^ 7)
+constexpr int kDppRowRor8 = 0x128;       // lane (i + 8) % 16 within 16 (lane ^ 8)
 // Value of lane ^ M (M = 1, 2, 4, 8) within each 16-lane row.
 template <int M>
 __device__ __forceinline__ float XorLane(float v) {
   if constexpr (M == 1) return Dpp<kDppQuadSwap1>(v);
   else if constexpr (M == 2) return Dpp<kDppQuadSwap2>(v);
   else if constexpr (M == 4) return Dpp<kDppQuadReverse>(Dpp<kDppRowHalfMirror>(v));  // (i ^ 7) ^ 3
-  else return Dpp<kDppRowHalfMirror>(Dpp<kDppRowMirror>(v));                          // (i ^ 15) ^ 7
+  else return Dpp<kDppRowRor8>(v);                                                  // (i + 8) % 16
 }
 
 // 128-point natural-order Sylvester butterfly, 16 lanes per block (a wave64 holds four
@@ -72,9 +53,22 @@ __device__ __forceinline__ float XorLane(float v) {
 // 1, 2, 4 are in-lane, strides 8..64 are lane xors 1..8 by DPP, in increasing order; each
 // output is lo + hi or lo - hi of the same two fp32 operands, so the values are those of
 // any evaluation of the same butterfly network.  All 64 lanes must be active.
-__device__ __forceinline__ void Wht128x8(float v[8]) {
+//
+// The cross-lane stages run in a signed form: lane j keeps sigma_j * value with
+// sigma_j = (-1)^popcount(j), so every stage is one fused multiply-add per value with the
+// partner's value (the DPP move folds into it): v = fma(partner, (j & M) ? -1 : 1, v).
+// The low lane gets sigma (lo + hi) and the high lane sigma (hi - lo) = -sigma (lo - hi),
+// which is what flips its sign.  Negation is exact and round-to-nearest is symmetric, so
+// every nonzero value equals the natural-order network's; an exactly-zero output may
+// carry the other sign of zero.  Callers fold WhtLaneSign() into the scale they apply
+// after the transform (a multiplication by +-1 is exact).
+__device__ __forceinline__ float WhtLaneSign() { return (__builtin_popcount(threadIdx.x & 15) & 1) ? -1.f : 1.f; }
+
+// In-lane butterfly stages of strides ST0, 2 ST0, ... < 8.
+template <int ST0>
+__device__ __forceinline__ void WhtInLane(float v[8]) {
 #pragma unroll
-  for (int st = 1; st < 8; st <<= 1)
+  for (int st = ST0; st < 8; st <<= 1)
 #pragma unroll
     for (int i = 0; i < 8; ++i)
       if (!(i & st)) {
@@ -82,20 +76,72 @@ __device__ __forceinline__ void Wht128x8(float v[8]) {
         v[i] = lo + hi;
         v[i + st] = lo - hi;
       }
-  const int j = threadIdx.x & 15;
-  auto stage = [&](auto mc) {
-    constexpr int M = decltype(mc)::value;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float o = XorLane<M>(v[i]);
-      v[i] = (j & M) ? (o - v[i]) : (v[i] + o);
-    }
-  };
-  stage(std::integral_constant<int, 1>{});
-  stage(std::integral_constant<int, 2>{});
-  stage(std::integral_constant<int, 4>{});
-  stage(std::integral_constant<int, 8>{});
 }
+
+// Cross-lane stages (strides 8..64) in the signed form.
+__device__ __forceinline__ void WhtCrossLaneSigned(float v[8]) {
+  const int j = threadIdx.x & 15;
+  // v_fmac_f32_dpp d, a, s: d += dpp(a) * s.  The compiler does not fold a DPP move into a
+  // multiply-add, so the stages are written out; each block starts with the two wait
+  // states a DPP read of a just-written VGPR needs.
+#define CX_WHT_FMAC8(DPP, A0, A1, A2, A3, A4, A5, A6, A7, ...)                                    \
+  asm volatile("s_nop 1\n"                                                                         \
+               "v_fmac_f32_dpp %0, " A0 ", %8 " DPP "\n"                                           \
+               "v_fmac_f32_dpp %1, " A1 ", %8 " DPP "\n"                                           \
+               "v_fmac_f32_dpp %2, " A2 ", %8 " DPP "\n"                                           \
+               "v_fmac_f32_dpp %3, " A3 ", %8 " DPP "\n"                                           \
+               "v_fmac_f32_dpp %4, " A4 ", %8 " DPP "\n"                                           \
+               "v_fmac_f32_dpp %5, " A5 ", %8 " DPP "\n"                                           \
+               "v_fmac_f32_dpp %6, " A6 ", %8 " DPP "\n"                                           \
+               "v_fmac_f32_dpp %7, " A7 ", %8 " DPP                                                 \
+               : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), \
+                 "+v"(v[7])                                                                        \
+               : "v"(sg), ##__VA_ARGS__)
+  // In place (a lane reads its partner's value before any lane writes): stages 1, 2, 8.
+#define CX_WHT_STAGE_INPLACE(DPP) CX_WHT_FMAC8(DPP, "%0", "%1", "%2", "%3", "%4", "%5", "%6", "%7")
+  {
+    const float sg = (j & 1) ? -1.f : 1.f;
+    CX_WHT_STAGE_INPLACE("quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf");
+  }
+  {
+    const float sg = (j & 2) ? -1.f : 1.f;
+    CX_WHT_STAGE_INPLACE("quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf");
+  }
+  {
+    float a[8];  // lane ^ 4 = (lane ^ 7) ^ 3: the first move by the compiler, the second folded
+#pragma unroll
+    for (int i = 0; i < 8; ++i) a[i] = Dpp<kDppRowHalfMirror>(v[i]);
+    const float sg = (j & 4) ? -1.f : 1.f;
+    CX_WHT_FMAC8("quad_perm:[3,2,1,0] row_mask:0xf bank_mask:0xf", "%9", "%10", "%11", "%12", "%13", "%14", "%15",
+                 "%16", "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(a[4]), "v"(a[5]), "v"(a[6]), "v"(a[7]));
+  }
+  {
+    const float sg = (j & 8) ? -1.f : 1.f;
+    CX_WHT_STAGE_INPLACE("row_ror:8 row_mask:0xf bank_mask:0xf");
+  }
+#undef CX_WHT_STAGE_INPLACE
+#undef CX_WHT_FMAC8
+}
+
+__device__ __forceinline__ void Wht128x8Signed(float v[8]) {
+  WhtInLane<1>(v);
+  WhtCrossLaneSigned(v);
+}
+
+// The same transform of 8 fp16 inputs packed in pairs (h[k] = elements 2k, 2k + 1): the
+// stride-1 stage is v_fma_mix_f32 lo * 1 + (+-hi), the fp32 sum of the two values with
+// one rounding, i.e. the conversion to fp32 folded into the first butterfly.
+__device__ __forceinline__ void Wht128x8SignedH(const uint32_t h[4], float v[8]) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    asm("v_fma_mix_f32 %0, %2, 1.0, %2 op_sel:[0,0,1] op_sel_hi:[1,0,1]\n"
+        "v_fma_mix_f32 %1, %2, 1.0, -%2 op_sel:[0,0,1] op_sel_hi:[1,0,1]"
+        : "=&v"(v[2 * k]), "=v"(v[2 * k + 1])
+        : "v"(h[k]));
+  WhtInLane<2>(v);
+  WhtCrossLaneSigned(v);
+}
+
 
 // Wave-uniform max / min by DPP row reductions and four lane reads.
 __device__ __forceinline__ float WaveMaxF(float v) {
@@ -172,8 +218,7 @@ __device__ __forceinline__ void StorePerm32x8(__half* d, const float v[8], float
   // Now h[q] is pair t of lane q: chunk t of the quad.
   *reinterpret_cast<int4*>(d + 32 * (j >> 2) + 8 * t) = make_int4(h[0], h[1], h[2], h[3]);
 }
-__device__ __forceinline__ void LoadH8(const __half* p, float v[8]) {
-  const uint4 u = *reinterpret_cast<const uint4*>(p);
+__device__ __forceinline__ void H8ToF(const uint4& u, float v[8]) {
   const __half2* h = reinterpret_cast<const __half2*>(&u);
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
@@ -181,6 +226,9 @@ __device__ __forceinline__ void LoadH8(const __half* p, float v[8]) {
     v[2 * k] = f.x;
     v[2 * k + 1] = f.y;
   }
+}
+__device__ __forceinline__ void LoadH8(const __half* p, float v[8]) {
+  H8ToF(*reinterpret_cast<const uint4*>(p), v);
 }
 __device__ __forceinline__ void LoadF8(const float* p, float v[8]) {
   const float4 a = *reinterpret_cast<const float4*>(p), b = *reinterpret_cast<const float4*>(p + 4);

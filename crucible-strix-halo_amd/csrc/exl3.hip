@@ -81,8 +81,8 @@ __global__ void __launch_bounds__(256) InputTransformKernel(XfInTable t) {
   LoadH8(J.suh + c0, s);
 #pragma unroll
   for (int i = 0; i < 8; ++i) v[i] = RoundH(v[i] * s[i]);
-  Wht128x8(v);
-  StorePerm32x8(J.xp + (size_t)r * J.I + blk * 128, v, kHadNorm);
+  Wht128x8Signed(v);
+  StorePerm32x8(J.xp + (size_t)r * J.I + blk * 128, v, kHadNorm * WhtLaneSign());
 }
 
 // Fixed-order sum of S K-segment partials, then the output transform, for a group of
@@ -108,15 +108,16 @@ __global__ void __launch_bounds__(256) OutputTransformKernel(XfOutTable t) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) v[i] = RoundH(v[i]);
   }
-  Wht128x8(v);
+  Wht128x8Signed(v);
   LoadH8(J.svh + c0, sv);
+  const float sg = WhtLaneSign();
   if (J.f16) {
     __half* d = static_cast<__half*>(J.y) + (size_t)r * J.ldy + c0;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) d[i] = __float2half(RoundH(v[i] * kHadNorm) * sv[i]);
+    for (int i = 0; i < 8; ++i) d[i] = __float2half(RoundH(v[i] * (sg * kHadNorm)) * sv[i]);
   } else {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] *= kHadNorm * sv[i];
+    for (int i = 0; i < 8; ++i) v[i] *= sg * (kHadNorm * sv[i]);
     StoreF8(static_cast<float*>(J.y) + (size_t)r * J.ldy + c0, v);
   }
 }

@@ -285,9 +285,9 @@ Exl3GemmKernel(GemmArgs g) {
         float v[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) v[i] = 0.f + ebuf[r][8 * j + i];
-        Wht128x8(v);
+        Wht128x8Signed(v);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] *= kHadNorm * sv[i];
+        for (int i = 0; i < 8; ++i) v[i] *= WhtLaneSign() * (kHadNorm * sv[i]);
         StoreF8(pl.y + (size_t)(row0 + r) * pl.ldy + c0, v);
       }
       return;
@@ -561,9 +561,9 @@ __global__ void __launch_bounds__(64 * WPG) Exl3GemmPrefillKernel(GemmArgs g) {
           float v[8];
 #pragma unroll
           for (int e = 0; e < 8; ++e) v[e] = 0.f + eb[rr][8 * j + e];
-          Wht128x8(v);
+          Wht128x8Signed(v);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) v[e] *= kHadNorm * sv[e];
+          for (int e = 0; e < 8; ++e) v[e] *= WhtLaneSign() * (kHadNorm * sv[e]);
           StoreF8(pl.y + (size_t)(row0 + r0 + rr) * pl.ldy + c0, v);
         }
         __syncthreads();

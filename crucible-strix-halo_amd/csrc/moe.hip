@@ -304,10 +304,10 @@ __global__ void __launch_bounds__(1024) GroupInputKernel(const int* __restrict__
       a[i] = RoundH(v[i] * s1[i]);
       v[i] = RoundH(v[i] * s2[i]);
     }
-    Wht128x8(a);
-    Wht128x8(v);
-    StorePerm32x8(xg + q * H + blk * 128, a, kHadNorm);
-    StorePerm32x8(xu + q * H + blk * 128, v, kHadNorm);
+    Wht128x8Signed(a);
+    Wht128x8Signed(v);
+    StorePerm32x8(xg + q * H + blk * 128, a, kHadNorm * WhtLaneSign());
+    StorePerm32x8(xu + q * H + blk * 128, v, kHadNorm * WhtLaneSign());
   }
 }
 
@@ -421,22 +421,40 @@ __global__ void __launch_bounds__(256) MoeInputKernel(const __half* __restrict__
   const __half* su = tb.up[e].suh;
   const int g = (threadIdx.x >> 4) & 3, j = threadIdx.x & 15;
   const __half* xr = x + (size_t)row * H;
-#pragma unroll 2
-  for (int blk = 4 * part + g; blk < H / 128; blk += 4 * S) {
-    const int c0 = blk * 128 + 8 * j;
-    float v[8], s1[8], s2[8], a[8];
-    LoadH8(xr + c0, v);
-    LoadH8(sg + c0, s1);
-    LoadH8(su + c0, s2);
+  const int nb = H / 128, st = 4 * S;
+  // Up to 4 blocks per lane group at a time: all their loads are issued before the first
+  // transform, so a wave keeps 12 16-byte loads in flight instead of 3.
+  for (int b0 = 4 * part + g; b0 < nb; b0 += 4 * st) {
+    uint4 rx[4], rg[4], ru[4];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      a[i] = RoundH(v[i] * s1[i]);
-      v[i] = RoundH(v[i] * s2[i]);
+    for (int it = 0; it < 4; ++it) {
+      const int c0 = (b0 + it * st) * 128 + 8 * j;
+      if (b0 + it * st < nb) {
+        rx[it] = *reinterpret_cast<const uint4*>(xr + c0);
+        rg[it] = *reinterpret_cast<const uint4*>(sg + c0);
+        ru[it] = *reinterpret_cast<const uint4*>(su + c0);
+      }
     }
-    Wht128x8(a);
-    Wht128x8(v);
-    StorePerm32x8(xg + (size_t)p * H + blk * 128, a, kHadNorm);
-    StorePerm32x8(xu + (size_t)p * H + blk * 128, v, kHadNorm);
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      const int blk = b0 + it * st;
+      if (blk >= nb) break;  // uniform over the 16-lane group
+      // RoundH(x * suh) is the fp16 product (an fp16 x fp16 product is exact in fp32).
+      const uint32_t hx[4] = {rx[it].x, rx[it].y, rx[it].z, rx[it].w};
+      const uint32_t hg[4] = {rg[it].x, rg[it].y, rg[it].z, rg[it].w};
+      const uint32_t hu[4] = {ru[it].x, ru[it].y, ru[it].z, ru[it].w};
+      uint32_t pa[4], pv[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        pa[k] = __builtin_bit_cast(uint32_t, __hmul2(__builtin_bit_cast(__half2, hx[k]), __builtin_bit_cast(__half2, hg[k])));
+        pv[k] = __builtin_bit_cast(uint32_t, __hmul2(__builtin_bit_cast(__half2, hx[k]), __builtin_bit_cast(__half2, hu[k])));
+      }
+      float a[8], v[8];
+      Wht128x8SignedH(pa, a);
+      Wht128x8SignedH(pv, v);
+      StorePerm32x8(xg + (size_t)p * H + blk * 128, a, kHadNorm * WhtLaneSign());
+      StorePerm32x8(xu + (size_t)p * H + blk * 128, v, kHadNorm * WhtLaneSign());
+    }
   }
 }
 
@@ -468,17 +486,18 @@ __global__ void __launch_bounds__(256) MoeMidKernel(const float* __restrict__ yg
       gv[i] = 0.f + gv[i];
       uv[i] = 0.f + uv[i];
     }
-    Wht128x8(gv);
-    Wht128x8(uv);
+    Wht128x8Signed(gv);
+    Wht128x8Signed(uv);
+    const float sg = WhtLaneSign();
     float v[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const float a = gv[i] * (kHadNorm * svg[i]);
-      const float b = uv[i] * (kHadNorm * svu[i]);
+      const float a = gv[i] * (sg * (kHadNorm * svg[i]));
+      const float b = uv[i] * (sg * (kHadNorm * svu[i]));
       v[i] = RoundH(RoundH(SiLU(a) * b) * sud[i]);
     }
-    Wht128x8(v);
-    StorePerm32x8(xd + (size_t)p * I + blk * 128, v, kHadNorm);
+    Wht128x8Signed(v);
+    StorePerm32x8(xd + (size_t)p * I + blk * 128, v, kHadNorm * sg);
   }
 }
 
