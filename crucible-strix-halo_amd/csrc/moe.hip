@@ -123,6 +123,14 @@ struct ExpertTables {
   const MatPtr* gate;  // [E + 1], index E = shared expert
   const MatPtr* up;
   const MatPtr* down;
+  // Packed copies of the scale vectors, expert-major ([E + 1][H] or [E + 1][I]): the
+  // transforms address them from the expert index alone, one dependent load fewer than
+  // through the pointer tables.
+  const __half* gate_suh;
+  const __half* up_suh;
+  const __half* gate_svh;
+  const __half* up_svh;
+  const __half* down_suh;
 };
 
 // ---- grouping --------------------------------------------------------------------------
@@ -297,8 +305,8 @@ __global__ void __launch_bounds__(1024) GroupInputKernel(const int* __restrict__
     const int c0 = blk * 128 + 8 * j;
     float v[8], s1[8], s2[8], a[8];
     LoadH8(xr + c0, v);
-    LoadH8(tb.gate[e].suh + c0, s1);
-    LoadH8(tb.up[e].suh + c0, s2);
+    LoadH8(tb.gate_suh + (size_t)e * H + c0, s1);
+    LoadH8(tb.up_suh + (size_t)e * H + c0, s2);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       a[i] = RoundH(v[i] * s1[i]);
@@ -400,7 +408,9 @@ __global__ void __launch_bounds__(1024) GroupScatterKernel(const int* __restrict
 // RoundH(x * suh) -> WHT128 -> * norm -> fp16 in MFMA row order.  S waves per compact
 // row: its route and expert are looked up once per wave, then lane group g (16 lanes) of
 // part t transforms the 128-blocks 4 t + g, 4 (t + S) + g, ... of both inputs (S = 1 for
-// long calls; short calls split rows for parallelism).  engine/layers/moe_rows.h:102-125.
+// long calls; short calls split rows for parallelism).  Compact-row order keeps the
+// writes sequential; walking routes in row order instead (reads shared, writes scattered
+// in 4 KB pieces) measured 8% slower.  engine/layers/moe_rows.h:102-125.
 __global__ void __launch_bounds__(256) MoeInputKernel(const __half* __restrict__ x, const int* __restrict__ rexp,
                                                       const int* __restrict__ rows, ExpertTables tb, int M, int topk,
                                                       int E, int H, int S, __half* __restrict__ xg,
@@ -417,8 +427,8 @@ __global__ void __launch_bounds__(256) MoeInputKernel(const __half* __restrict__
     row = p - M * topk;
     e = E;
   }
-  const __half* sg = tb.gate[e].suh;
-  const __half* su = tb.up[e].suh;
+  const __half* sg = tb.gate_suh + (size_t)e * H;
+  const __half* su = tb.up_suh + (size_t)e * H;
   const int g = (threadIdx.x >> 4) & 3, j = threadIdx.x & 15;
   const __half* xr = x + (size_t)row * H;
   const int nb = H / 128, st = 4 * S;
@@ -427,10 +437,12 @@ __global__ void __launch_bounds__(256) MoeInputKernel(const __half* __restrict__
   for (int b0 = 4 * part + g; b0 < nb; b0 += 4 * st) {
     uint4 rx[4], rg[4], ru[4];
 #pragma unroll
+    for (int it = 0; it < 4; ++it)
+      if (b0 + it * st < nb) rx[it] = *reinterpret_cast<const uint4*>(xr + (b0 + it * st) * 128 + 8 * j);
+#pragma unroll
     for (int it = 0; it < 4; ++it) {
       const int c0 = (b0 + it * st) * 128 + 8 * j;
       if (b0 + it * st < nb) {
-        rx[it] = *reinterpret_cast<const uint4*>(xr + c0);
         rg[it] = *reinterpret_cast<const uint4*>(sg + c0);
         ru[it] = *reinterpret_cast<const uint4*>(su + c0);
       }
@@ -469,9 +481,9 @@ __global__ void __launch_bounds__(256) MoeMidKernel(const float* __restrict__ yg
   const int p = blockIdx.x * 4 + (int)(threadIdx.x >> 6);
   if (p >= P) return;  // whole waves
   const int e = p < M * topk ? __builtin_amdgcn_readfirstlane(rexp[p]) : E;
-  const __half* svg_p = tb.gate[e].svh;
-  const __half* svu_p = tb.up[e].svh;
-  const __half* sud_p = tb.down[e].suh;
+  const __half* svg_p = tb.gate_svh + (size_t)e * I;
+  const __half* svu_p = tb.up_svh + (size_t)e * I;
+  const __half* sud_p = tb.down_suh + (size_t)e * I;
   const int g = (threadIdx.x >> 4) & 3, j = threadIdx.x & 15;
   for (int blk = g; blk < I / 128; blk += 4) {
     const int c0 = blk * 128 + 8 * j;
@@ -558,6 +570,7 @@ struct cx_moe_plan {
   int k2_gu, cb_gu, k2_d, cb_d;      // routed experts
   int k2_sgu, cb_sgu, k2_sd, cb_sd;  // shared expert
   cx::MatPtr* d_tables;              // device: gate[E+1], up[E+1], down[E+1]
+  __half* d_scales;                  // device: packed scale copies (ExpertTables)
   cx::ExpertTables tb;
   hipEvent_t* trace;                 // caller's events (nullable), recorded between stages
   int n_trace, trace_cursor;
@@ -802,7 +815,36 @@ int cx_moe_plan_create(const cx_moe_layer* layer, cx_moe_plan** out) {
     delete pl;
     return (int)err;
   }
-  pl->tb = ExpertTables{pl->d_tables, pl->d_tables + n, pl->d_tables + 2 * n};
+  // Packed scale copies: gate suh, up suh [E+1][H]; gate svh, up svh, down suh [E+1][I].
+  const size_t nsc = n * (2 * (size_t)H + 3 * (size_t)I);
+  err = hipMalloc(&pl->d_scales, nsc * sizeof(__half));
+  __half* g_suh = pl->d_scales;
+  __half* u_suh = g_suh + n * H;
+  __half* g_svh = u_suh + n * H;
+  __half* u_svh = g_svh + n * I;
+  __half* d_suh = u_svh + n * I;
+  for (int e = 0; e <= E && err == hipSuccess; ++e) {
+    const cx_moe_expert& ex = e < E ? layer->experts[e] : layer->shared;
+    const struct {
+      __half* dst;
+      const void* src;
+      int len;
+    } cp[5] = {{g_suh + (size_t)e * H, ex.gate.suh, H},
+               {u_suh + (size_t)e * H, ex.up.suh, H},
+               {g_svh + (size_t)e * I, ex.gate.svh, I},
+               {u_svh + (size_t)e * I, ex.up.svh, I},
+               {d_suh + (size_t)e * I, ex.down.suh, I}};
+    for (const auto& c : cp)
+      if (err == hipSuccess) err = hipMemcpyAsync(c.dst, c.src, (size_t)c.len * sizeof(__half), hipMemcpyDefault, nullptr);
+  }
+  if (err == hipSuccess) err = hipStreamSynchronize(nullptr);
+  if (err != hipSuccess) {
+    if (pl->d_scales) (void)hipFree(pl->d_scales);
+    (void)hipFree(pl->d_tables);
+    delete pl;
+    return (int)err;
+  }
+  pl->tb = ExpertTables{pl->d_tables, pl->d_tables + n, pl->d_tables + 2 * n, g_suh, u_suh, g_svh, u_svh, d_suh};
   *out = pl;
   return CX_OK;
 }
@@ -810,6 +852,7 @@ int cx_moe_plan_create(const cx_moe_layer* layer, cx_moe_plan** out) {
 void cx_moe_plan_destroy(cx_moe_plan* plan) {
   if (!plan) return;
   if (plan->d_tables) (void)hipFree(plan->d_tables);
+  if (plan->d_scales) (void)hipFree(plan->d_scales);
   std::free(plan->trace);
   delete plan;
 }

@@ -151,7 +151,9 @@ typedef struct cx_moe_layer {
 } cx_moe_layer;
 
 /* Prepared (device-resident) expert tables of a layer: built once, reused by every
- * call.  Replaces the d_experts upload (engine/model/flashnext/model.h:75). */
+ * call.  Replaces the d_experts upload (engine/model/flashnext/model.h:75).  The plan
+ * keeps packed device copies of every expert's suh / svh vectors taken at creation
+ * (2 H + 3 I halves per expert); the tiles are referenced, not copied.  Synchronous. */
 typedef struct cx_moe_plan cx_moe_plan;
 int cx_moe_plan_create(const cx_moe_layer* layer, cx_moe_plan** plan);
 void cx_moe_plan_destroy(cx_moe_plan* plan);
