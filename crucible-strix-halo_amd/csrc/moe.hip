@@ -334,13 +334,18 @@ __global__ void __launch_bounds__(1024) GroupCountKernel(const int* __restrict__
   for (int e = threadIdx.x; e < E; e += blockDim.x) tile_counts[(size_t)e * ntiles + blockIdx.x] = h[e];
 }
 
-// One workgroup: exclusive scan of tile_counts in (expert, tile) order -> tile bases,
-// counts, offsets and the GEMM entries.
-__global__ void __launch_bounds__(1024) GroupScanKernel(int* __restrict__ tile_counts, int ntiles, GroupOut o) {
+// Scan and scatter in one launch, one workgroup per tile: every workgroup reads all tile
+// histograms (ntiles x E counts, a few tens of KB from L2) and scans them itself in
+// (expert, tile) order for its own tile bases, so no separate scan launch has to finish
+// first.  Workgroup 0 also writes counts, offsets and the GEMM entries.  Then a stable
+// in-tile scatter.
+__global__ void __launch_bounds__(1024) GroupScatterKernel(const int* __restrict__ sel,
+                                                           const int* __restrict__ tile_counts, int ntiles,
+                                                           GroupOut o) {
   __shared__ int s_scan[128];
-  __shared__ int s_cnt[kMaxExperts];
-  const int e = threadIdx.x;
-  int cnt = 0;
+  __shared__ int s_cur[kMaxExperts];
+  const int e = threadIdx.x, tile = blockIdx.x;
+  int cnt = 0, before = 0;
   if (e < o.E) {
     // Independent loads issued 8 at a time (a dependent chain would wait ntiles times).
     const int* tc = tile_counts + (size_t)e * ntiles;
@@ -350,56 +355,42 @@ __global__ void __launch_bounds__(1024) GroupScanKernel(int* __restrict__ tile_c
 #pragma unroll
       for (int i = 0; i < 8; ++i) v[i] = tc[t + i];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) cnt += v[i];
-    }
-    for (; t < ntiles; ++t) cnt += tc[t];
-  }
-  int total = 0, ctotal = 0;
-  const int off = BlockExclusiveScan(cnt, s_scan, &total);
-  const int nch = o.entries ? (cnt + o.chunk - 1) / o.chunk : 0;
-  const int chb = BlockExclusiveScan(nch, s_scan, &ctotal);
-  if (e < o.E) {
-    s_cnt[e] = cnt;
-    o.counts[e] = cnt;
-    o.offsets[e] = off;
-    int run = off;
-    int* tc = tile_counts + (size_t)e * ntiles;
-    int t = 0;
-    for (; t + 8 <= ntiles; t += 8) {
-      int v[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) v[i] = tc[t + i];
-#pragma unroll
       for (int i = 0; i < 8; ++i) {
-        tc[t + i] = run;
-        run += v[i];
+        before += t + i < tile ? v[i] : 0;
+        cnt += v[i];
       }
     }
     for (; t < ntiles; ++t) {
-      const int c = tc[t];
-      tc[t] = run;
-      run += c;
+      const int v = tc[t];
+      before += t < tile ? v : 0;
+      cnt += v;
     }
-    if (o.entries) WriteEntries(o, e, chb, cnt, off);
   }
-  if (e == 0) o.offsets[o.E] = total;
-  if (o.entries) {
-    WriteSharedEntries(o, threadIdx.x, blockDim.x);
-    if (threadIdx.x == 0) *o.n_entries = (o.M + o.chunk - 1) / o.chunk + ctotal;
-    FillEmptyEntries(o, (o.M + o.chunk - 1) / o.chunk + ctotal);
+  int total = 0;
+  const int off = BlockExclusiveScan(cnt, s_scan, &total);
+  if (e < o.E) s_cur[e] = off + before;
+  if (tile == 0) {
+    int ctotal = 0;
+    const int nch = o.entries ? (cnt + o.chunk - 1) / o.chunk : 0;
+    const int chb = BlockExclusiveScan(nch, s_scan, &ctotal);
+    if (e < o.E) {
+      o.counts[e] = cnt;
+      o.offsets[e] = off;
+      if (o.entries) WriteEntries(o, e, chb, cnt, off);
+    }
+    if (e == 0) o.offsets[o.E] = total;
+    if (o.entries) {
+      WriteSharedEntries(o, threadIdx.x, blockDim.x);
+      if (threadIdx.x == 0) *o.n_entries = (o.M + o.chunk - 1) / o.chunk + ctotal;
+      FillEmptyEntries(o, (o.M + o.chunk - 1) / o.chunk + ctotal);
+    }
   }
-}
-
-__global__ void __launch_bounds__(1024) GroupScatterKernel(const int* __restrict__ sel, const int* __restrict__ tile_base,
-                                                           int ntiles, GroupOut o) {
-  __shared__ int s_cur[kMaxExperts];
-  const int n = o.M * o.topk;
-  for (int e = threadIdx.x; e < o.E; e += blockDim.x) s_cur[e] = tile_base[(size_t)e * ntiles + blockIdx.x];
   __syncthreads();
-  const int i = blockIdx.x * kTile + threadIdx.x;
-  const int e = i < n ? sel[i] : -1;
-  const int p = StableAppend(e, s_cur, min((int)blockDim.x, n - (int)blockIdx.x * kTile + 63) >> 6);
-  if (p >= 0) WritePair(o, p, i, e);
+  const int n = o.M * o.topk;
+  const int i = tile * kTile + threadIdx.x;
+  const int se = i < n ? sel[i] : -1;
+  const int p = StableAppend(se, s_cur, min((int)blockDim.x, n - tile * kTile + 63) >> 6);
+  if (p >= 0) WritePair(o, p, i, se);
 }
 
 // ---- activation transforms of the experts ----------------------------------------------
@@ -666,7 +657,6 @@ int LaunchGroup(const int* sel, GroupOut& o, int* tile_counts, int ntiles, hipSt
     hipLaunchKernelGGL(GroupSmallKernel, dim3(1), dim3(1024), 0, s, sel, o);
   } else {
     hipLaunchKernelGGL(GroupCountKernel, dim3(ntiles), dim3(1024), 0, s, sel, n, o.E, ntiles, tile_counts);
-    hipLaunchKernelGGL(GroupScanKernel, dim3(1), dim3(1024), 0, s, tile_counts, ntiles, o);
     hipLaunchKernelGGL(GroupScatterKernel, dim3(ntiles), dim3(1024), 0, s, sel, tile_counts, ntiles, o);
   }
   return LaunchStatus();
