@@ -332,30 +332,8 @@ __device__ __forceinline__ GridPos XcdEntryMajor() {
 // tile of a step (16 NRBT rows x 32 inputs) is loaded once into LDS and shared by the
 // waves, so more waves per workgroup read the activations fewer times.  One barrier per
 // step double-buffers the activation tile.
-#ifdef CX_WG_TIMES
-__device__ ulonglong2 g_wg_times[1 << 16];
-__device__ unsigned g_wg_xcc[1 << 16];
-#endif
 template <int K2, int CB, int NRBT, int CPWV, int WPG>
 __global__ void __launch_bounds__(64 * WPG) Exl3GemmPrefillKernel(GemmArgs g) {
-#ifdef CX_WG_TIMES
-  const unsigned long long wt0 = __builtin_amdgcn_s_memrealtime();
-  struct WgTimeRec {
-    unsigned long long t0;
-    __device__ ~WgTimeRec() {
-      if (threadIdx.x == 0) {
-        const unsigned id = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
-        unsigned xcc;
-        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
-        const unsigned k = id + (gridDim.z == 2 ? 0u : (1u << 15));
-        if (id < (1u << 15)) {
-          g_wg_times[k] = make_ulonglong2(t0, __builtin_amdgcn_s_memrealtime());
-          g_wg_xcc[k] = xcc;
-        }
-      }
-    }
-  } wrec{wt0};
-#endif
   constexpr int T = TileDwords(K2);
   constexpr int SD = 4 * T;
   constexpr int DPL = (SD + 63) / 64;

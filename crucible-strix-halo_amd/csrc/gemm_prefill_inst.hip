@@ -37,14 +37,3 @@ bool CX_CAT(LaunchGemmPrefillRate, CX_RATE)(int cb, int nrbt, int wpg, dim3 grid
 }
 
 }  // namespace cx
-#ifdef CX_WG_TIMES
-extern "C" int cx_debug_wg_times(void* times, void* xcc, int n) {
-  if (hipMemcpyFromSymbol(times, HIP_SYMBOL(cx::g_wg_times), sizeof(ulonglong2) * n) != hipSuccess) return 1;
-  if (hipMemcpyFromSymbol(xcc, HIP_SYMBOL(cx::g_wg_xcc), sizeof(unsigned) * n) != hipSuccess) return 1;
-  return 0;
-}
-extern "C" int cx_debug_wg_clear() {
-  static ulonglong2 z[1 << 16];
-  return hipMemcpyToSymbol(HIP_SYMBOL(cx::g_wg_times), z, sizeof(z)) != hipSuccess;
-}
-#endif
