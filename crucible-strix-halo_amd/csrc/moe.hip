@@ -337,8 +337,8 @@ __global__ void __launch_bounds__(1024) GroupCountKernel(const int* __restrict__
 // Scan and scatter in one launch, one workgroup per tile: every workgroup reads all tile
 // histograms (ntiles x E counts, a few tens of KB from L2) and scans them itself in
 // (expert, tile) order for its own tile bases, so no separate scan launch has to finish
-// first.  Workgroup 0 also writes counts, offsets and the GEMM entries.  Then a stable
-// in-tile scatter.
+// first, then does a stable in-tile scatter.  One extra workgroup (index ntiles) writes
+// counts, offsets and the GEMM entries meanwhile.
 __global__ void __launch_bounds__(1024) GroupScatterKernel(const int* __restrict__ sel,
                                                            const int* __restrict__ tile_counts, int ntiles,
                                                            GroupOut o) {
@@ -369,7 +369,7 @@ __global__ void __launch_bounds__(1024) GroupScatterKernel(const int* __restrict
   int total = 0;
   const int off = BlockExclusiveScan(cnt, s_scan, &total);
   if (e < o.E) s_cur[e] = off + before;
-  if (tile == 0) {
+  if (tile == ntiles) {  // the extra workgroup: counts, offsets, entries
     int ctotal = 0;
     const int nch = o.entries ? (cnt + o.chunk - 1) / o.chunk : 0;
     const int chb = BlockExclusiveScan(nch, s_scan, &ctotal);
@@ -384,6 +384,7 @@ __global__ void __launch_bounds__(1024) GroupScatterKernel(const int* __restrict
       if (threadIdx.x == 0) *o.n_entries = (o.M + o.chunk - 1) / o.chunk + ctotal;
       FillEmptyEntries(o, (o.M + o.chunk - 1) / o.chunk + ctotal);
     }
+    return;
   }
   __syncthreads();
   const int n = o.M * o.topk;
@@ -657,7 +658,7 @@ int LaunchGroup(const int* sel, GroupOut& o, int* tile_counts, int ntiles, hipSt
     hipLaunchKernelGGL(GroupSmallKernel, dim3(1), dim3(1024), 0, s, sel, o);
   } else {
     hipLaunchKernelGGL(GroupCountKernel, dim3(ntiles), dim3(1024), 0, s, sel, n, o.E, ntiles, tile_counts);
-    hipLaunchKernelGGL(GroupScatterKernel, dim3(ntiles), dim3(1024), 0, s, sel, tile_counts, ntiles, o);
+    hipLaunchKernelGGL(GroupScatterKernel, dim3(ntiles + 1), dim3(1024), 0, s, sel, tile_counts, ntiles, o);
   }
   return LaunchStatus();
 }
