@@ -310,6 +310,43 @@ int cx_exl3_dequant(const cx_exl3_matrix* m, uint16_t* w_hat, cx_stream_t stream
   return LaunchStatus();
 }
 
+int cx_exl3_input_transform(const cx_exl3_matrix* m, const void* x, int32_t x_dtype, int32_t ldx, int32_t M,
+                            uint16_t* xh, cx_stream_t stream) {
+  int rc = CheckMatrix(m);
+  if (rc) return rc;
+  if (!x || !xh) return CX_E_ARG;
+  if (x_dtype != CX_F16 && x_dtype != CX_F32) return CX_E_ARG;
+  if (M <= 0 || ldx < m->in_features || ldx % 8) return CX_E_SHAPE;
+  XfInTable t{};
+  t.n = 1;
+  t.M = M;
+  t.job[0] = XfIn{x, reinterpret_cast<const __half*>(m->suh), reinterpret_cast<__half*>(xh), ldx, m->in_features,
+                  x_dtype == CX_F32 ? 1 : 0, 0};
+  const long items = (long)M * (m->in_features / 128);
+  hipLaunchKernelGGL(InputTransformKernel, dim3((unsigned)((items * 16 + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, t);
+  return LaunchStatus();
+}
+
+int cx_exl3_output_transform(const cx_exl3_matrix* m, const float* y_raw, int32_t M, void* y, int32_t y_dtype,
+                             cx_stream_t stream) {
+  int rc = CheckMatrix(m);
+  if (rc) return rc;
+  if (!y_raw || !y) return CX_E_ARG;
+  if (y_dtype != CX_F16 && y_dtype != CX_F32) return CX_E_ARG;
+  if (M <= 0) return CX_E_SHAPE;
+  const int O = m->out_features;
+  XfOutTable t{};
+  t.n = 1;
+  t.M = M;
+  t.job[0] = XfOut{y_raw, (long long)M * O, reinterpret_cast<const __half*>(m->svh), y, 1, O, O,
+                   y_dtype == CX_F16 ? 1 : 0, 0};
+  const long items = (long)M * (O / 128);
+  hipLaunchKernelGGL(OutputTransformKernel, dim3((unsigned)((items * 16 + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, t);
+  return LaunchStatus();
+}
+
 size_t cx_exl3_linear_workspace_size(const cx_exl3_matrix* m, int32_t M) {
   if (CheckMatrix(m) || M <= 0) return 0;
   const LinearPlan p = PlanLinear(m->in_features, m->out_features, M);

@@ -20,7 +20,8 @@ ERRORS = {-1: "invalid argument", -2: "invalid shape", -3: "unsupported bitrate"
           -5: "expert id out of range", -6: "unsupported combination", -7: "checkpoint format error"}
 
 EXPORTED = [
-    "cx_exl3_tile_bytes", "cx_exl3_repack", "cx_exl3_dequant", "cx_exl3_linear_workspace_size", "cx_exl3_linear",
+    "cx_exl3_tile_bytes", "cx_exl3_repack", "cx_exl3_dequant", "cx_exl3_input_transform",
+    "cx_exl3_output_transform", "cx_exl3_linear_workspace_size", "cx_exl3_linear",
     "cx_exl3_group_workspace_size", "cx_exl3_group",
     "cx_dense_linear", "cx_moe_route", "cx_moe_group_workspace_size", "cx_moe_group", "cx_moe_plan_create", "cx_moe_plan_destroy",
     "cx_moe_layer_workspace_size", "cx_moe_layer_forward", "cx_moe_layer_forward_hc", "cx_moe_plan_set_trace",
@@ -72,6 +73,8 @@ def lib() -> ctypes.CDLL:
         L.cx_exl3_tile_bytes.restype = SZ
         L.cx_exl3_repack.argtypes = [P, I32, I32, I32, P, P]
         L.cx_exl3_dequant.argtypes = [ctypes.POINTER(Matrix), P, P]
+        L.cx_exl3_input_transform.argtypes = [ctypes.POINTER(Matrix), P, I32, I32, I32, P, P]
+        L.cx_exl3_output_transform.argtypes = [ctypes.POINTER(Matrix), P, I32, P, I32, P]
         L.cx_exl3_linear_workspace_size.argtypes = [ctypes.POINTER(Matrix), I32]
         L.cx_exl3_linear_workspace_size.restype = SZ
         L.cx_exl3_linear.argtypes = [ctypes.POINTER(Matrix), P, I32, P, I32, P, I32, P, SZ, P]
@@ -107,7 +110,7 @@ def lib() -> ctypes.CDLL:
         L.cx_exl3_load_linear.argtypes = [P, ctypes.c_char_p, ctypes.POINTER(Matrix), P, P, P, P, SZ, P]
         L.cx_last_error.restype = ctypes.c_char_p
         L.cx_version.restype = ctypes.c_char_p
-        for fn in ("cx_exl3_repack", "cx_exl3_dequant", "cx_exl3_linear", "cx_exl3_group", "cx_dense_linear", "cx_moe_route", "cx_moe_group",
+        for fn in ("cx_exl3_repack", "cx_exl3_dequant", "cx_exl3_input_transform", "cx_exl3_output_transform", "cx_exl3_linear", "cx_exl3_group", "cx_dense_linear", "cx_moe_route", "cx_moe_group",
                    "cx_moe_plan_create", "cx_moe_layer_forward", "cx_moe_layer_forward_hc", "cx_checkpoint_open",
                    "cx_checkpoint_tensor", "cx_exl3_linear_info", "cx_exl3_load_linear"):
             getattr(L, fn).restype = ctypes.c_int

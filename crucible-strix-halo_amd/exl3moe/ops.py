@@ -50,6 +50,24 @@ class DeviceLinear:
         check("cx_exl3_dequant", lib().cx_exl3_dequant(ctypes.byref(self.struct), ptr(w), stream_ptr(stream)))
         return w
 
+    def input_transform(self, x: torch.Tensor, stream=None) -> torch.Tensor:
+        """xh fp16 [M][I] in the library's MFMA row order (cx_exl3_input_transform)."""
+        assert x.dtype in (torch.float16, torch.float32) and x.stride(1) == 1 and x.shape[1] >= self.in_features
+        xh = torch.empty(x.shape[0], self.in_features, dtype=torch.float16, device=x.device)
+        check("cx_exl3_input_transform", lib().cx_exl3_input_transform(
+            ctypes.byref(self.struct), ptr(x), CX_F32 if x.dtype == torch.float32 else CX_F16, x.stride(0),
+            x.shape[0], ptr(xh), stream_ptr(stream)))
+        return xh
+
+    def output_transform(self, y_raw: torch.Tensor, out_dtype=torch.float32, stream=None) -> torch.Tensor:
+        """WHT128(y_raw) * (norm * svh) per 128-block (cx_exl3_output_transform)."""
+        assert y_raw.dtype == torch.float32 and y_raw.is_contiguous() and y_raw.shape[1] == self.out_features
+        y = torch.empty(y_raw.shape[0], self.out_features, dtype=out_dtype, device=y_raw.device)
+        check("cx_exl3_output_transform", lib().cx_exl3_output_transform(
+            ctypes.byref(self.struct), ptr(y_raw), y_raw.shape[0], ptr(y),
+            CX_F16 if out_dtype == torch.float16 else CX_F32, stream_ptr(stream)))
+        return y
+
     def workspace_size(self, M: int) -> int:
         return int(lib().cx_exl3_linear_workspace_size(ctypes.byref(self.struct), M))
 

@@ -66,6 +66,24 @@ int cx_exl3_repack(const int16_t* trellis, int32_t in_features, int32_t out_feat
  * parity hook for ref/exl3_ref.py:110-119 `reconstruct_inner`. */
 int cx_exl3_dequant(const cx_exl3_matrix* m, uint16_t* w_hat, cx_stream_t stream);
 
+/* The input transform of a linear alone: per 128-block of each row, xh =
+ * fp16(WHT128(RoundH(RoundH(x) * suh)) * norm), written in this library's MFMA row order
+ * (natural element e of a 128-block at position 32 (e >> 5) + p(e & 31), p(r) =
+ * 8 ((r & 7) >> 1) + 4 (r >> 4) + (r & 1) + 2 ((r >> 3) & 1)).  The parity hook for
+ * LinInKernel / LinInLane (engine/exl3/exl3.h:48-65, 96-102) and hadamard_kernel with
+ * pre_scale (ref/exl3_ref.py:140-156): it runs the kernel cx_exl3_linear uses.
+ *   x   fp16 (CX_F16) or fp32 (CX_F32) [M][ldx], ldx >= in_features, ldx % 8 == 0
+ *   xh  fp16 [M][in_features] */
+int cx_exl3_input_transform(const cx_exl3_matrix* m, const void* x, int32_t x_dtype, int32_t ldx, int32_t M,
+                            uint16_t* xh, cx_stream_t stream);
+
+/* The output transform alone: y = WHT128(y_raw) * (norm * svh) in fp32 (CX_F32, the
+ * engine's LinOutBlock, engine/exl3/exl3.h:69-82) or fp16(RoundH(WHT128(RoundH(y_raw)) *
+ * norm) * svh) (CX_F16, ref/exl3_ref.py:153-156, 175), per 128-block.  The parity hook for
+ * the output transform cx_exl3_linear runs.  y_raw fp32 [M][out_features]; y [M][out_features]. */
+int cx_exl3_output_transform(const cx_exl3_matrix* m, const float* y_raw, int32_t M, void* y, int32_t y_dtype,
+                             cx_stream_t stream);
+
 /* y = EXL3 linear of M packed activation rows.  Replaces `Build` + `RunGroup`
  * (engine/engine.hip:1046, 1731) over one `LinJob` with R = M rows, i.e. LinInKernel
  * -> split-K GEMV -> LinOutKernel (engine/exl3/exl3.h:48-82, 330-389).

@@ -184,3 +184,74 @@ def test_linear_group_errors(ops):
     assert lib().cx_exl3_group(jobs, 1, 4, None, 0, ws.data_ptr(), ws.numel(), None) == -1
     jobs[0].x_dtype = 0
     assert lib().cx_exl3_group(jobs, 1, 4, None, 0, ws.data_ptr(), 16, None) == -4
+
+
+def _natural_order(xh):
+    # The library's MFMA row order: natural element e of a 128-block sits at
+    # 32 (e >> 5) + p(e & 31) (the header's p); gather it back to natural order.
+    r = np.arange(32)
+    p = 8 * ((r & 7) >> 1) + 4 * (r >> 4) + (r & 1) + 2 * ((r >> 3) & 1)
+    n = xh.shape[1]
+    e = np.arange(n)
+    return xh[:, (e // 32) * 32 + p[e % 32]]
+
+
+def _same_values(got, want):
+    # Bitwise on every nonzero value; an exactly-zero output may carry either sign of zero.
+    got = np.asarray(got)
+    want = np.asarray(want)
+    np.testing.assert_array_equal(got, want)  # +0 == -0
+    nz = want != 0
+    bits = np.uint16 if got.dtype == np.float16 else np.uint32
+    np.testing.assert_array_equal(got[nz].view(bits), want[nz].view(bits))
+
+
+def _plain_linear(ops, I, O, suh, svh):
+    # Transforms read only suh / svh: the tiles are a zero buffer of the right size.
+    t = torch.zeros(I * O * 8 // 16 // 4, dtype=torch.int32, device="cuda")
+    return ops.DeviceLinear(t, torch.from_numpy(suh).cuda(), torch.from_numpy(svh).cuda(), I, O, 8)
+
+
+def test_input_transform_bit_exact(ops):
+    # The input transform kernel of cx_exl3_linear against the oracle's fp16 Hadamard
+    # with pre-scale (ref/exl3_ref.py:140-156), fp16 and fp32 inputs, general fp16 suh.
+    rng = np.random.default_rng(21)
+    I = 512
+    suh = (rng.standard_normal(I) * 1.5).astype(np.float16)
+    lin = _plain_linear(ops, I, 256, suh, np.ones(256, np.float16))
+    x = (rng.standard_normal((9, I)) * np.array([1, 1e-3, 30, 1, 1, 1, 1, 1, 1])[:, None]).astype(np.float16)
+    x[3] = 0
+    x[4, ::3] = 0
+    want = O.hadamard(x, pre=suh)
+    got = _natural_order(lin.input_transform(torch.from_numpy(x).cuda()).cpu().numpy())
+    _same_values(got, want)
+    # fp32 rows (a strided view): RoundH(x) first.
+    xf = np.zeros((5, I + 64), np.float32)
+    xf[:, :I] = rng.standard_normal((5, I)).astype(np.float32)
+    got = _natural_order(lin.input_transform(torch.from_numpy(xf).cuda()[:, :I]).cpu().numpy())
+    _same_values(got, O.hadamard(xf[:, :I].astype(np.float16), pre=suh))
+
+
+def test_output_transform_bit_exact(ops):
+    # fp32 output: WHT128(y) * (norm * svh).  With svh a power of two the two products
+    # round alike whatever the association, so the oracle's (WHT(y) * norm) * svh is
+    # bitwise the expected value; general svh within one rounding.
+    rng = np.random.default_rng(22)
+    O_ = 384
+    y = (rng.standard_normal((7, O_)) * 10).astype(np.float32)
+    y[2] = 0
+    svh_p2 = (rng.choice([0.5, 1.0, 2.0], O_) * rng.choice([-1, 1], O_)).astype(np.float16)
+    lin = _plain_linear(ops, 128, O_, np.ones(128, np.float16), svh_p2)
+    got = lin.output_transform(torch.from_numpy(y).cuda()).cpu().numpy()
+    want = O.hadamard(y) * svh_p2.astype(np.float32)
+    _same_values(got, want)
+    svh = (rng.standard_normal(O_) + 0.1).astype(np.float16)
+    lin = _plain_linear(ops, 128, O_, np.ones(128, np.float16), svh)
+    got = lin.output_transform(torch.from_numpy(y).cuda()).cpu().numpy()
+    want = (O.hadamard(y).astype(np.float64) * svh.astype(np.float64))
+    np.testing.assert_allclose(got, want, rtol=2.5e-7, atol=0)
+    # fp16 output: fp16(RoundH(WHT(RoundH(y)) * norm) * svh).
+    got = lin.output_transform(torch.from_numpy(y).cuda(), torch.float16).cpu().numpy()
+    yh = y.astype(np.float16).astype(np.float32)
+    want = (O.hadamard(yh).astype(np.float16).astype(np.float32) * svh.astype(np.float32)).astype(np.float16)
+    _same_values(got, want)
