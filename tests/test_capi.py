@@ -47,6 +47,12 @@ def test_argument_errors_without_gpu():
     assert L.cx_exl3_tile_bytes(2048, 512, 8) == 2048 * 512 * 4 // 8
     m = exl3moe.Matrix(1, 1, 1, 2048, 512, 8, 2)
     assert L.cx_exl3_linear_workspace_size(ctypes.byref(m), 1) > 0
+    # transform hooks: stride, dtype and row checks come before any launch
+    assert L.cx_exl3_input_transform(ctypes.byref(m), ctypes.c_void_p(1), 1, 2040, 3, ctypes.c_void_p(1), None) == -2
+    assert L.cx_exl3_input_transform(ctypes.byref(m), ctypes.c_void_p(1), 7, 2048, 3, ctypes.c_void_p(1), None) == -1
+    assert L.cx_exl3_input_transform(ctypes.byref(m), None, 1, 2048, 3, ctypes.c_void_p(1), None) == -1
+    assert L.cx_exl3_output_transform(ctypes.byref(m), ctypes.c_void_p(1), 0, ctypes.c_void_p(1), 1, None) == -2
+    assert L.cx_exl3_output_transform(ctypes.byref(m), ctypes.c_void_p(1), 2, ctypes.c_void_p(1), 5, None) == -1
     # rows must match the session offsets
     ro = exl3moe.i32_host([0, 2, 5])
     assert L.cx_exl3_linear(ctypes.byref(m), ctypes.c_void_p(1), 4, ro, 2, ctypes.c_void_p(1), 1,
