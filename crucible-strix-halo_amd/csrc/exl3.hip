@@ -70,18 +70,28 @@ __global__ void __launch_bounds__(256) InputTransformKernel(XfInTable t) {
   if (local >= t.M * nb) return;  // whole 16-lane groups
   const int r = local / nb, blk = local % nb, j = threadIdx.x & 15;
   const int c0 = blk * 128 + 8 * j;
-  float v[8], s[8];
+  // x as 4 packed fp16 pairs (fp32 sources rounded), times suh in fp16 (the fp16
+  // product is RoundH of the exact fp32 product), into the transform's first stage.
+  uint32_t h[4];
   if (J.xf32) {
-    LoadF8(static_cast<const float*>(J.x) + (size_t)r * J.ldx + c0, v);
+    float f[8];
+    LoadF8(static_cast<const float*>(J.x) + (size_t)r * J.ldx + c0, f);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = RoundH(v[i]);
+    for (int k = 0; k < 4; ++k) h[k] = __builtin_bit_cast(uint32_t, __floats2half2_rn(f[2 * k], f[2 * k + 1]));
   } else {
-    LoadH8(static_cast<const __half*>(J.x) + (size_t)r * J.ldx + c0, v);
+    const uint4 u = *reinterpret_cast<const uint4*>(static_cast<const __half*>(J.x) + (size_t)r * J.ldx + c0);
+    h[0] = u.x;
+    h[1] = u.y;
+    h[2] = u.z;
+    h[3] = u.w;
   }
-  LoadH8(J.suh + c0, s);
+  const uint4 su = *reinterpret_cast<const uint4*>(J.suh + c0);
+  const uint32_t hs[4] = {su.x, su.y, su.z, su.w};
 #pragma unroll
-  for (int i = 0; i < 8; ++i) v[i] = RoundH(v[i] * s[i]);
-  Wht128x8Signed(v);
+  for (int k = 0; k < 4; ++k)
+    h[k] = __builtin_bit_cast(uint32_t, __hmul2(__builtin_bit_cast(__half2, h[k]), __builtin_bit_cast(__half2, hs[k])));
+  float v[8];
+  Wht128x8SignedH(h, v);
   StorePerm32x8(J.xp + (size_t)r * J.I + blk * 128, v, kHadNorm * WhtLaneSign());
 }
 

@@ -274,6 +274,24 @@ __global__ void __launch_bounds__(1024) GroupSmallKernel(const int* __restrict__
   GroupSmallBody(sel, o, s_cur, s_scan);
 }
 
+// The gate and up input transforms of one lane's 8 elements of a 128-block (signed
+// form, before the norm): x, suh_gate, suh_up as 8 packed fp16 each.  RoundH(x * suh) is
+// the fp16 product (an fp16 x fp16 product is exact in fp32, so one fp16 rounding).
+__device__ __forceinline__ void InputPairTransform(const uint4& x, const uint4& sg, const uint4& su, float a[8],
+                                                   float v[8]) {
+  const uint32_t hx[4] = {x.x, x.y, x.z, x.w};
+  const uint32_t hg[4] = {sg.x, sg.y, sg.z, sg.w};
+  const uint32_t hu[4] = {su.x, su.y, su.z, su.w};
+  uint32_t pa[4], pv[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    pa[k] = __builtin_bit_cast(uint32_t, __hmul2(__builtin_bit_cast(__half2, hx[k]), __builtin_bit_cast(__half2, hg[k])));
+    pv[k] = __builtin_bit_cast(uint32_t, __hmul2(__builtin_bit_cast(__half2, hx[k]), __builtin_bit_cast(__half2, hu[k])));
+  }
+  Wht128x8SignedH(pa, a);
+  Wht128x8SignedH(pv, v);
+}
+
 // Decode: grouping and the gate/up input transforms in one launch, after routing.
 // Workgroup 0 groups all rows (GroupSmallBody); the other workgroups, a few per row, write
 // the gate and up input transforms (engine/exl3/exl3.h:48-65: RoundH(x * suh) -> WHT128 ->
@@ -303,17 +321,10 @@ __global__ void __launch_bounds__(1024) GroupInputKernel(const int* __restrict__
     const int e = s_e[slot];
     const size_t q = slot < topk ? (size_t)row * topk + slot : (size_t)M * topk + row;
     const int c0 = blk * 128 + 8 * j;
-    float v[8], s1[8], s2[8], a[8];
-    LoadH8(xr + c0, v);
-    LoadH8(tb.gate_suh + (size_t)e * H + c0, s1);
-    LoadH8(tb.up_suh + (size_t)e * H + c0, s2);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      a[i] = RoundH(v[i] * s1[i]);
-      v[i] = RoundH(v[i] * s2[i]);
-    }
-    Wht128x8Signed(a);
-    Wht128x8Signed(v);
+    float a[8], v[8];
+    InputPairTransform(*reinterpret_cast<const uint4*>(xr + c0),
+                       *reinterpret_cast<const uint4*>(tb.gate_suh + (size_t)e * H + c0),
+                       *reinterpret_cast<const uint4*>(tb.up_suh + (size_t)e * H + c0), a, v);
     StorePerm32x8(xg + q * H + blk * 128, a, kHadNorm * WhtLaneSign());
     StorePerm32x8(xu + q * H + blk * 128, v, kHadNorm * WhtLaneSign());
   }
@@ -443,19 +454,8 @@ __global__ void __launch_bounds__(256) MoeInputKernel(const __half* __restrict__
     for (int it = 0; it < 4; ++it) {
       const int blk = b0 + it * st;
       if (blk >= nb) break;  // uniform over the 16-lane group
-      // RoundH(x * suh) is the fp16 product (an fp16 x fp16 product is exact in fp32).
-      const uint32_t hx[4] = {rx[it].x, rx[it].y, rx[it].z, rx[it].w};
-      const uint32_t hg[4] = {rg[it].x, rg[it].y, rg[it].z, rg[it].w};
-      const uint32_t hu[4] = {ru[it].x, ru[it].y, ru[it].z, ru[it].w};
-      uint32_t pa[4], pv[4];
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        pa[k] = __builtin_bit_cast(uint32_t, __hmul2(__builtin_bit_cast(__half2, hx[k]), __builtin_bit_cast(__half2, hg[k])));
-        pv[k] = __builtin_bit_cast(uint32_t, __hmul2(__builtin_bit_cast(__half2, hx[k]), __builtin_bit_cast(__half2, hu[k])));
-      }
       float a[8], v[8];
-      Wht128x8SignedH(pa, a);
-      Wht128x8SignedH(pv, v);
+      InputPairTransform(rx[it], rg[it], ru[it], a, v);
       StorePerm32x8(xg + (size_t)p * H + blk * 128, a, kHadNorm * WhtLaneSign());
       StorePerm32x8(xu + (size_t)p * H + blk * 128, v, kHadNorm * WhtLaneSign());
     }
