@@ -44,7 +44,7 @@ def expert_bytes(k2_gu, k2_d):
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--layers", type=int, default=3, help="seeded layers the steps rotate over (cold reads)")
     ap.add_argument("--prefill-steps", type=int, default=6)
@@ -54,6 +54,8 @@ def parse():
     ap.add_argument("--no-long", action="store_true", help="skip the config-5 long prefill + output head")
     ap.add_argument("--no-stream", action="store_true", help="skip the device-copy HBM stream measurement")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--min-warmup-s", type=float, default=0.5,
+                    help="the untimed warmup also runs until this much wall time has passed (GPU clocks settle)")
     ap.add_argument("--seed", type=int, default=2024)
     ap.add_argument("--host-data", action="store_true",
                     help="generate the layers with numpy on the host (no torch kernels in the process)")
@@ -84,9 +86,12 @@ def make_batches(n, seed, prefill=False):
     return out
 
 
-def run_workload(plans, batches, warmup, steps, mode):
-    """Times `steps` layer calls after `warmup` (no instrumentation in the timed loop), then
-    repeats the same calls with the library's stage events to get per-stage times."""
+def run_workload(plans, batches, warmup, steps, mode, min_warm_s=0.0):
+    """Times `steps` layer calls after `warmup` untimed calls (no instrumentation in the
+    timed loop), then repeats the same calls with the library's stage events to get
+    per-stage times.  The warmup also continues until `min_warm_s` seconds of calls have
+    run: the GPU's clocks take a few hundred milliseconds of sustained load to settle, and
+    a handful of 0.1 ms steps would time the ramp instead of the steady state."""
     import torch
     from exl3moe.trace import StageTrace
     maxM = max(b[0][-1] for b in batches)
@@ -100,9 +105,15 @@ def run_workload(plans, batches, warmup, steps, mode):
         plans[i % len(plans)](x, lg, row_offsets=offs, mode=mode, workspace=ws, y=ys[:offs[-1]], sel=sels[b])
         return b
 
-    for i in range(warmup):
-        call(i)
+    w0 = time.perf_counter()
+    nwarm = 0
+    while nwarm < warmup or time.perf_counter() - w0 < min_warm_s:
+        call(nwarm)
+        nwarm += 1
+        if nwarm % 32 == 0:
+            torch.cuda.synchronize()  # keep the host within a few steps of the GPU
     torch.cuda.synchronize()
+    # The timed steps continue the same sequence as if exactly `warmup` steps had run.
     t0 = time.perf_counter()
     order = [call(warmup + s) for s in range(steps)]
     torch.cuda.synchronize()
@@ -126,7 +137,7 @@ def run_workload(plans, batches, warmup, steps, mode):
     rows = sum(batches[b][0][-1] for b in order)
     used = [len(set(sels[b].cpu().numpy().ravel().tolist())) for b in order]
     return {"wall_s": wall, "rows": rows, "stages": stage_rows, "distinct": used,
-            "M": [batches[b][0][-1] for b in order]}
+            "M": [batches[b][0][-1] for b in order], "warmup_run": nwarm}
 
 
 def graph_decode(plans, batches, warmup, steps, mode):
@@ -410,7 +421,7 @@ def main():
     eb = expert_bytes(k2, k2)
     nb = max(args.steps, 8)
     batches = make_batches(nb, args.seed + 100)
-    r = run_workload(plans, batches, args.warmup, args.steps, CX_MOE_DECODE)
+    r = run_workload(plans, batches, args.warmup, args.steps, CX_MOE_DECODE, args.min_warmup_s)
     ms_step = r["wall_s"] * 1000 / args.steps
     tok_s = r["rows"] / r["wall_s"]
     st = np.array(r["stages"])  # [steps][7] ms
@@ -437,6 +448,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "warmup_steps_run": r["warmup_run"],
         "ms_per_step": round(ms_step, 4),
         "higher_is_better": True,
         "scaling": "weak",
@@ -461,7 +473,7 @@ def main():
         out["graph"] = {"tokens_per_s": round(r["rows"] / (gms * args.steps / 1000), 1), "ms_per_step": round(gms, 4)}
     if not args.no_prefill:
         pb = make_batches(2, args.seed + 200, prefill=True)
-        rp = run_workload(plans, pb, 2, args.prefill_steps, CX_MOE_PREFILL)
+        rp = run_workload(plans, pb, 2, args.prefill_steps, CX_MOE_PREFILL, args.min_warmup_s)
         stp = np.array(rp["stages"])
         ms_p = rp["wall_s"] * 1000 / args.prefill_steps
         flops = 2.0 * (TOPK + 1) * 2048 * 3 * H * IE
