@@ -289,3 +289,22 @@ def test_config5_output_head(ops):
         ts = np.ascontiguousarray(tr[:, c0 // 16:(c0 + 256) // 16])
         ref = O.matvec(x, O.reconstruct_inner(ts, 6), suh, svh[c0:c0 + 256], np.float32)
         assert rel_l2(y[:, c0:c0 + 256], ref) <= 1e-3
+
+
+@pytest.mark.parametrize("mode", [1, 2])
+def test_many_experts_layer(ops, mode):
+    # E = 600 > 512 (the 16-per-lane router), k = 16: decode (fused group + transforms) and
+    # prefill paths on small matrices.
+    from exl3moe import synth
+    plan = synth.device_moe_layer(17, E=600, H=256, Ie=128, topk=16)
+    rng = np.random.default_rng(19)
+    for M in (3, 40):
+        x = rng.standard_normal((M, 256)).astype(np.float16)
+        lg = rng.standard_normal((M, 601)).astype(np.float32)
+        y, sel, wts = run_layer(plan, x, lg, mode)
+        rs, rw = O.route(lg, 600, 16)
+        np.testing.assert_array_equal(sel, rs)
+        ref = oracle_layer(plan, x, rs, rw)
+        e = rel_l2(y, ref)
+        print(f"E=600 k=16 mode={mode} M={M} rel_l2={e:.3e}")
+        assert e <= 1e-3
