@@ -3,14 +3,19 @@
  *
  * Drop-in boundary for Crucible's EXL3 linear op and MoE layer (the reference is the
  * engine's in-process C++: file:line citations are relative to the reference root).
- * All pointers are device pointers unless a parameter says "host".  Every call is
- * asynchronous on the given HIP stream, allocates nothing (workspace is caller
+ * All pointers are device pointers unless a parameter says "host".  Every compute call
+ * is asynchronous on the given HIP stream, allocates nothing (workspace is caller
  * memory, sized by the matching *_workspace_size query), never exits, and returns:
  *     0  success
  *    <0  invalid argument or shape (CX_E_*)
  *    >0  a hipError_t from a launch
  *
  * fp16 data is passed as uint16_t bit patterns (IEEE binary16).
+ *
+ * The exceptions are set-up calls: cx_moe_plan_create / _destroy allocate and free the
+ * plan's device tables (synchronously), and the checkpoint reader does host I/O.  One
+ * host thread drives a plan at a time (its trace ring is plan state), as one host
+ * thread owns the reference engine (engine/serve/README.md:13-14).
  */
 #ifndef CRUCIBLE_EXL3_H
 #define CRUCIBLE_EXL3_H
