@@ -230,6 +230,19 @@ __device__ __forceinline__ void H8ToF(const uint4& u, float v[8]) {
 __device__ __forceinline__ void LoadH8(const __half* p, float v[8]) {
   H8ToF(*reinterpret_cast<const uint4*>(p), v);
 }
+// 8 consecutive activations at element idx of x as packed fp16: fp16 sources as they
+// are, fp32 sources rounded to nearest-even (RoundH of each value).  16- / 32-byte loads.
+__device__ __forceinline__ uint4 LoadAsH8(const void* x, bool f32, size_t idx) {
+  if (f32) {
+    const float* p = static_cast<const float*>(x) + idx;
+    const float4 a = *reinterpret_cast<const float4*>(p), b = *reinterpret_cast<const float4*>(p + 4);
+    return make_uint4(__builtin_bit_cast(uint32_t, __floats2half2_rn(a.x, a.y)),
+                      __builtin_bit_cast(uint32_t, __floats2half2_rn(a.z, a.w)),
+                      __builtin_bit_cast(uint32_t, __floats2half2_rn(b.x, b.y)),
+                      __builtin_bit_cast(uint32_t, __floats2half2_rn(b.z, b.w)));
+  }
+  return *reinterpret_cast<const uint4*>(static_cast<const __half*>(x) + idx);
+}
 __device__ __forceinline__ void LoadF8(const float* p, float v[8]) {
   const float4 a = *reinterpret_cast<const float4*>(p), b = *reinterpret_cast<const float4*>(p + 4);
   v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;

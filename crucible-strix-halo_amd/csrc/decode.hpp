@@ -6,16 +6,17 @@
 // position i holds the 16-bit state ending at the end of symbol i; position i = 8t + j
 // is element (2(t%4) + (j&1) + 8((j>>1)&1), t/4 + 8(j>>2)) of the tile.
 //
-// Lane mapping.  A wave processes a pair of horizontally adjacent tiles (same 16 input
-// rows, 32 output columns) per step with two v_mfma_f32_16x16x16_f16.  MFMA lane L
-// (column n = L % 16, k-group q = L / 16) decodes run t = 4 (n % 8) + q of tile
-// n / 8: the 8 consecutive positions 8t..8t+7.  Positions 8t..8t+3 are column n % 8
-// at rows {2q, 2q+1, 2q+8, 2q+9} (the first MFMA's B operand) and 8t+4..8t+7 are the
-// same rows of column n % 8 + 8 (the second MFMA's).  Activations are stored with the
-// matching row order (PermPos16), so no decoded weight ever crosses lanes.
+// Lane mapping.  A wave processes a step of two k-tiles of a column pair (32 input rows,
+// 32 output columns: 4 tiles) with two v_mfma_f32_16x16x32_f16.  MFMA lane L (column
+// n = L % 16, k-group q = L / 16) decodes run t = 4 (n % 8) + q of column tile n / 8 in
+// both k-tiles: the 8 consecutive positions 8t..8t+7.  Positions 8t..8t+3 are column
+// n % 8 at rows {2q, 2q+1, 2q+8, 2q+9} and 8t+4..8t+7 the same rows of column n % 8 + 8;
+// the first four of each k-tile form the first MFMA's B operand (8 halves), the second
+// four the second's.  Activations are stored in the matching 32-row order (PermPos32 in
+// common.hpp), so no decoded weight ever crosses lanes.
 //
 // A run needs the 16 - d bits before it (its first state's history): the lane reads
-// the (at most 3) dwords that hold its window, at lane-invariant offsets.
+// the (at most 3) dwords that hold its window, at offsets fixed per lane.
 #pragma once
 
 #include "common.hpp"

@@ -270,6 +270,7 @@ int CheckJob(const cx_exl3_job& j) {
   if ((j.x_dtype != CX_F16 && j.x_dtype != CX_F32) || (j.y_dtype != CX_F16 && j.y_dtype != CX_F32)) return CX_E_ARG;
   // Rows are read and written in 16- / 32-byte pieces.
   if (j.ldx < j.m.in_features || j.ldy < j.m.out_features || j.ldx % 8 || j.ldy % 8) return CX_E_SHAPE;
+  if (reinterpret_cast<uintptr_t>(j.x) % 16 || reinterpret_cast<uintptr_t>(j.y) % 16) return CX_E_SHAPE;
   return CX_OK;
 }
 
@@ -363,16 +364,16 @@ size_t cx_exl3_linear_workspace_size(const cx_exl3_matrix* m, int32_t M) {
   return LinearWorkspace(p, m->in_features, m->out_features, M);
 }
 
-int cx_exl3_linear(const cx_exl3_matrix* m, const uint16_t* x, int32_t M, const int32_t* row_offsets,
-                   int32_t n_sessions, void* y, int32_t y_dtype, void* workspace, size_t workspace_bytes,
-                   cx_stream_t stream) {
+int cx_exl3_linear(const cx_exl3_matrix* m, const void* x, int32_t x_dtype, int32_t ldx, int32_t M,
+                   const int32_t* row_offsets, int32_t n_sessions, void* y, int32_t y_dtype, void* workspace,
+                   size_t workspace_bytes, cx_stream_t stream) {
   int rc = CheckMatrix(m);
   if (rc) return rc;
   if (!x || !y || !workspace) return CX_E_ARG;
   if (M <= 0) return CX_E_SHAPE;
-  if (y_dtype != CX_F16 && y_dtype != CX_F32) return CX_E_ARG;
   if ((rc = RowOffsetsCheck(row_offsets, n_sessions, M))) return rc;
-  const cx_exl3_job job{*m, x, CX_F16, m->in_features, y, y_dtype, m->out_features};
+  const cx_exl3_job job{*m, x, x_dtype, ldx, y, y_dtype, m->out_features};
+  if ((rc = CheckJob(job))) return rc;
   if (workspace_bytes < GroupWorkspace(&job, 1, M)) return CX_E_WORKSPACE;
   return RunGroup(&job, 1, M, static_cast<char*>(workspace), (hipStream_t)stream);
 }

@@ -224,6 +224,9 @@ __device__ int StableAppend(int e, int* cursor, int nw) {
   return valid ? base + rank : -1;
 }
 
+// An expert id in [0, E), or -1 for an id outside it (such a route is dropped).
+__device__ __forceinline__ int ValidExpert(int e, int E) { return (unsigned)e < (unsigned)E ? e : -1; }
+
 __device__ void WritePair(const GroupOut& o, int p, int i, int e) {
   o.pairs[p] = i;
   o.row_ids[p] = i / o.topk;
@@ -237,7 +240,10 @@ __device__ void GroupSmallBody(const int* sel, const GroupOut& o, int* s_cur, in
   const int n = o.M * o.topk;
   for (int e = threadIdx.x; e < o.E; e += blockDim.x) s_cur[e] = 0;
   __syncthreads();
-  for (int i = threadIdx.x; i < n; i += blockDim.x) atomicAdd(&s_cur[sel[i]], 1);  // counts only
+  for (int i = threadIdx.x; i < n; i += blockDim.x) {  // counts only; ids outside [0, E) are dropped
+    const int e = sel[i];
+    if ((unsigned)e < (unsigned)o.E) atomicAdd(&s_cur[e], 1);
+  }
   __syncthreads();
   const int e = threadIdx.x;
   const int cnt = e < o.E ? s_cur[e] : 0;
@@ -262,7 +268,7 @@ __device__ void GroupSmallBody(const int* sel, const GroupOut& o, int* s_cur, in
   __syncthreads();
   for (int base = 0; base < n; base += blockDim.x) {
     const int i = base + threadIdx.x;
-    const int e = i < n ? sel[i] : -1;
+    const int e = i < n ? ValidExpert(sel[i], o.E) : -1;
     const int p = StableAppend(e, s_cur, min((int)blockDim.x, n - base + 63) >> 6);
     if (p >= 0) WritePair(o, p, i, e);
   }
@@ -299,8 +305,9 @@ __device__ __forceinline__ void InputPairTransform(const uint4& x, const uint4& 
 // route order: row r * k + slot, shared expert row M k + r.  The transforms need only the
 // row's own selection, so the workgroups are independent; the gate/up GEMM gathers its
 // compact rows through pairs[].
-__global__ void __launch_bounds__(1024) GroupInputKernel(const int* __restrict__ sel, const __half* __restrict__ x,
-                                                         ExpertTables tb, int H, __half* __restrict__ xg,
+__global__ void __launch_bounds__(1024) GroupInputKernel(const int* __restrict__ sel, const void* __restrict__ x,
+                                                         int xf32, long long ldx, ExpertTables tb, int H,
+                                                         __half* __restrict__ xg,
                                                          __half* __restrict__ xu, GroupOut o) {
   __shared__ int s_e[kMaxTopK + 1];
   __shared__ int s_cur[kMaxExperts];
@@ -315,14 +322,14 @@ __global__ void __launch_bounds__(1024) GroupInputKernel(const int* __restrict__
   const int row = (blockIdx.x - 1) / wpr, part = (blockIdx.x - 1) % wpr;
   if ((int)threadIdx.x <= topk) s_e[threadIdx.x] = (int)threadIdx.x < topk ? sel[(size_t)row * topk + threadIdx.x] : o.E;
   __syncthreads();
-  const __half* xr = x + (size_t)row * H;
+  const size_t xr = (size_t)row * ldx;
   for (int it = part * per + (threadIdx.x >> 4); it < min(items, (part + 1) * per); it += per) {
     const int slot = it / nb, blk = it % nb;
     const int e = s_e[slot];
     const size_t q = slot < topk ? (size_t)row * topk + slot : (size_t)M * topk + row;
     const int c0 = blk * 128 + 8 * j;
     float a[8], v[8];
-    InputPairTransform(*reinterpret_cast<const uint4*>(xr + c0),
+    InputPairTransform(LoadAsH8(x, xf32, xr + c0),
                        *reinterpret_cast<const uint4*>(tb.gate_suh + (size_t)e * H + c0),
                        *reinterpret_cast<const uint4*>(tb.up_suh + (size_t)e * H + c0), a, v);
     StorePerm32x8(xg + q * H + blk * 128, a, kHadNorm * WhtLaneSign());
@@ -340,7 +347,10 @@ __global__ void __launch_bounds__(1024) GroupCountKernel(const int* __restrict__
   for (int e = threadIdx.x; e < E; e += blockDim.x) h[e] = 0;
   __syncthreads();
   const int i = blockIdx.x * kTile + threadIdx.x;
-  if (i < n) atomicAdd(&h[sel[i]], 1);  // counts only; never decides order
+  if (i < n) {  // counts only; never decides order
+    const int e = ValidExpert(sel[i], E);
+    if (e >= 0) atomicAdd(&h[e], 1);
+  }
   __syncthreads();
   for (int e = threadIdx.x; e < E; e += blockDim.x) tile_counts[(size_t)e * ntiles + blockIdx.x] = h[e];
 }
@@ -400,7 +410,7 @@ __global__ void __launch_bounds__(1024) GroupScatterKernel(const int* __restrict
   __syncthreads();
   const int n = o.M * o.topk;
   const int i = tile * kTile + threadIdx.x;
-  const int se = i < n ? sel[i] : -1;
+  const int se = i < n ? ValidExpert(sel[i], o.E) : -1;
   const int p = StableAppend(se, s_cur, min((int)blockDim.x, n - tile * kTile + 63) >> 6);
   if (p >= 0) WritePair(o, p, i, se);
 }
@@ -414,7 +424,8 @@ __global__ void __launch_bounds__(1024) GroupScatterKernel(const int* __restrict
 // long calls; short calls split rows for parallelism).  Compact-row order keeps the
 // writes sequential; walking routes in row order instead (reads shared, writes scattered
 // in 4 KB pieces) measured 8% slower.  engine/layers/moe_rows.h:102-125.
-__global__ void __launch_bounds__(256) MoeInputKernel(const __half* __restrict__ x, const int* __restrict__ rexp,
+__global__ void __launch_bounds__(256) MoeInputKernel(const void* __restrict__ x, int xf32, long long ldx,
+                                                      const int* __restrict__ rexp,
                                                       const int* __restrict__ rows, ExpertTables tb, int M, int topk,
                                                       int E, int H, int S, __half* __restrict__ xg,
                                                       __half* __restrict__ xu) {
@@ -433,7 +444,7 @@ __global__ void __launch_bounds__(256) MoeInputKernel(const __half* __restrict__
   const __half* sg = tb.gate_suh + (size_t)e * H;
   const __half* su = tb.up_suh + (size_t)e * H;
   const int g = (threadIdx.x >> 4) & 3, j = threadIdx.x & 15;
-  const __half* xr = x + (size_t)row * H;
+  const size_t xr = (size_t)row * ldx;
   const int nb = H / 128, st = 4 * S;
   // Up to 4 blocks per lane group at a time: all their loads are issued before the first
   // transform, so a wave keeps 12 16-byte loads in flight instead of 3.
@@ -441,7 +452,7 @@ __global__ void __launch_bounds__(256) MoeInputKernel(const __half* __restrict__
     uint4 rx[4], rg[4], ru[4];
 #pragma unroll
     for (int it = 0; it < 4; ++it)
-      if (b0 + it * st < nb) rx[it] = *reinterpret_cast<const uint4*>(xr + (b0 + it * st) * 128 + 8 * j);
+      if (b0 + it * st < nb) rx[it] = LoadAsH8(x, xf32, xr + (b0 + it * st) * 128 + 8 * j);
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
       const int c0 = (b0 + it * st) * 128 + 8 * j;
@@ -857,12 +868,16 @@ size_t cx_moe_layer_workspace_size(const cx_moe_plan* plan, int32_t M, int32_t m
 
 namespace cx {
 
-int MoeForward(const cx_moe_plan* pl, const uint16_t* x, const float* logits, int32_t ld, const float* shared_logit,
+int MoeForward(const cx_moe_plan* pl, const void* x, int32_t x_dtype, int32_t ldx, const float* logits, int32_t ld,
+               const float* shared_logit,
                int32_t M, const int32_t* row_offsets, int32_t n_sessions, float* y, const HcArgs* hc, int32_t* sel_out,
                float* wts_out, int32_t mode, void* workspace, size_t workspace_bytes, cx_stream_t stream) {
   if (!pl || !x || !logits || (!y && !hc) || !workspace) return CX_E_ARG;
   if (mode < CX_MOE_AUTO || mode > CX_MOE_PREFILL) return CX_E_ARG;
+  if (x_dtype != CX_F16 && x_dtype != CX_F32) return CX_E_ARG;
   if (M <= 0) return CX_E_SHAPE;
+  // Rows are read in 16- / 32-byte pieces.
+  if (ldx < pl->H || ldx % 8 || reinterpret_cast<uintptr_t>(x) % 16) return CX_E_SHAPE;
   if (ld < pl->E || (!shared_logit && ld < pl->E + 1)) return CX_E_SHAPE;
   int rc;
   if ((rc = RowOffsetsCheck(row_offsets, n_sessions, M))) return rc;
@@ -904,8 +919,8 @@ int MoeForward(const cx_moe_plan* pl, const uint16_t* x, const float* logits, in
     // Grouping and input transforms in one launch; the trace records it as the group
     // stage (input stage empty).
     const int wpr = ((pl->topk + 1) * (pl->H / 128) + 63) / 64;
-    hipLaunchKernelGGL(GroupInputKernel, dim3(1 + M * wpr), dim3(1024), 0, s, sel, reinterpret_cast<const __half*>(x),
-                       pl->tb, pl->H, xg, xu, o);
+    hipLaunchKernelGGL(GroupInputKernel, dim3(1 + M * wpr), dim3(1024), 0, s, sel, x, (int)(x_dtype == CX_F32),
+                       (long long)ldx, pl->tb, pl->H, xg, xu, o);
     mark();
   } else {
     if ((rc = LaunchGroup(sel, o, tiles, sz.ntiles, s))) return rc;
@@ -913,7 +928,8 @@ int MoeForward(const cx_moe_plan* pl, const uint16_t* x, const float* logits, in
     // Split rows over more waves when there are few of them (decode).
     const int S = sz.P >= 4096 ? 1 : std::max(1, std::min(4, pl->H / 512));
     hipLaunchKernelGGL(MoeInputKernel, dim3((unsigned)(((long)sz.P * S + 3) / 4)), dim3(256), 0, s,
-                       reinterpret_cast<const __half*>(x), rexp, rows, pl->tb, M, pl->topk, pl->E, pl->H, S, xg, xu);
+                       x, (int)(x_dtype == CX_F32), (long long)ldx, rexp, rows, pl->tb, M, pl->topk, pl->E, pl->H, S,
+                       xg, xu);
   }
   mark();
   if (!LaunchExpertGemm(pl, sz, true, xg, xu, yg, yu, ent, nent, front ? pairs : nullptr, s)) return CX_E_UNSUPPORTED;
@@ -942,23 +958,25 @@ int MoeForward(const cx_moe_plan* pl, const uint16_t* x, const float* logits, in
 
 extern "C" {
 
-int cx_moe_layer_forward(const cx_moe_plan* pl, const uint16_t* x, const float* logits, int32_t ld,
-                         const float* shared_logit, int32_t M, const int32_t* row_offsets, int32_t n_sessions, float* y,
-                         int32_t* sel, float* wts, int32_t mode, void* workspace, size_t workspace_bytes,
-                         cx_stream_t stream) {
+int cx_moe_layer_forward(const cx_moe_plan* pl, const void* x, int32_t x_dtype, int32_t ldx, const float* logits,
+                         int32_t ld, const float* shared_logit, int32_t M, const int32_t* row_offsets,
+                         int32_t n_sessions, float* y, int32_t* sel, float* wts, int32_t mode, void* workspace,
+                         size_t workspace_bytes, cx_stream_t stream) {
   if (!y) return CX_E_ARG;
-  return MoeForward(pl, x, logits, ld, shared_logit, M, row_offsets, n_sessions, y, nullptr, sel, wts, mode, workspace,
+  return MoeForward(pl, x, x_dtype, ldx, logits, ld, shared_logit, M, row_offsets, n_sessions, y, nullptr, sel, wts, mode, workspace,
                     workspace_bytes, stream);
 }
 
-int cx_moe_layer_forward_hc(const cx_moe_plan* pl, const uint16_t* x, const float* logits, int32_t ld,
-                            const float* shared_logit, int32_t M, const int32_t* row_offsets, int32_t n_sessions,
+int cx_moe_layer_forward_hc(const cx_moe_plan* pl, const void* x, int32_t x_dtype, int32_t ldx,
+                            const float* logits, int32_t ld, const float* shared_logit, int32_t M, const int32_t* row_offsets, int32_t n_sessions,
                             const float* post, int32_t n_streams, float* H, int64_t ldh, int32_t* sel, float* wts,
                             int32_t mode, void* workspace, size_t workspace_bytes, cx_stream_t stream) {
   if (!pl || !post || !H) return CX_E_ARG;
   if (n_streams < 1 || n_streams > 64 || ldh < (int64_t)n_streams * pl->H) return CX_E_SHAPE;
+  // The combine reads and writes H in 16-byte pieces.
+  if (ldh % 4 || reinterpret_cast<uintptr_t>(H) % 16) return CX_E_SHAPE;
   const HcArgs hc{post, H, (long long)ldh, n_streams};
-  return MoeForward(pl, x, logits, ld, shared_logit, M, row_offsets, n_sessions, nullptr, &hc, sel, wts, mode,
+  return MoeForward(pl, x, x_dtype, ldx, logits, ld, shared_logit, M, row_offsets, n_sessions, nullptr, &hc, sel, wts, mode,
                     workspace, workspace_bytes, stream);
 }
 

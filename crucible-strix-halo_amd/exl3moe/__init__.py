@@ -77,7 +77,7 @@ def lib() -> ctypes.CDLL:
         L.cx_exl3_output_transform.argtypes = [ctypes.POINTER(Matrix), P, I32, P, I32, P]
         L.cx_exl3_linear_workspace_size.argtypes = [ctypes.POINTER(Matrix), I32]
         L.cx_exl3_linear_workspace_size.restype = SZ
-        L.cx_exl3_linear.argtypes = [ctypes.POINTER(Matrix), P, I32, P, I32, P, I32, P, SZ, P]
+        L.cx_exl3_linear.argtypes = [ctypes.POINTER(Matrix), P, I32, I32, I32, P, I32, P, I32, P, SZ, P]
         L.cx_exl3_group_workspace_size.argtypes = [ctypes.POINTER(Job), I32, I32]
         L.cx_exl3_group_workspace_size.restype = SZ
         L.cx_exl3_group.argtypes = [ctypes.POINTER(Job), I32, I32, P, I32, P, SZ, P]
@@ -91,9 +91,9 @@ def lib() -> ctypes.CDLL:
         L.cx_moe_plan_destroy.restype = None
         L.cx_moe_layer_workspace_size.argtypes = [P, I32, I32]
         L.cx_moe_layer_workspace_size.restype = SZ
-        L.cx_moe_layer_forward.argtypes = [P, P, P, I32, P, I32, P, I32, P, P, P, I32, P, SZ, P]
-        L.cx_moe_layer_forward_hc.argtypes = [P, P, P, I32, P, I32, P, I32, P, I32, P, ctypes.c_int64, P, P, I32, P,
-                                              SZ, P]
+        L.cx_moe_layer_forward.argtypes = [P, P, I32, I32, P, I32, P, I32, P, I32, P, P, P, I32, P, SZ, P]
+        L.cx_moe_layer_forward_hc.argtypes = [P, P, I32, I32, P, I32, P, I32, P, I32, P, I32, P, ctypes.c_int64, P,
+                                              P, I32, P, SZ, P]
         L.cx_moe_plan_set_trace.argtypes = [P, ctypes.POINTER(ctypes.c_void_p), I32]
         L.cx_moe_plan_set_trace.restype = ctypes.c_int
         I64P = ctypes.POINTER(ctypes.c_int64)

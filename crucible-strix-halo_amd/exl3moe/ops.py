@@ -16,6 +16,11 @@ from . import (CX_CB, CX_F16, CX_F32, CX_MOE_AUTO, Expert, Layer, Matrix, check,
                stream_ptr)
 
 
+def _xdtype(x: torch.Tensor) -> int:
+    """CX_F16 / CX_F32 of an activation tensor."""
+    return CX_F32 if x.dtype == torch.float32 else CX_F16
+
+
 def _dev(a: np.ndarray, device="cuda") -> torch.Tensor:
     return torch.from_numpy(np.ascontiguousarray(a)).to(device)
 
@@ -80,14 +85,15 @@ class DeviceLinear:
 
     def forward_into(self, x, y, row_offsets=None, workspace=None, stream=None):
         M = x.shape[0]
-        assert x.dtype == torch.float16 and x.is_contiguous() and x.shape[1] == self.in_features
+        assert x.dtype in (torch.float16, torch.float32) and x.stride(1) == 1 and x.shape[1] >= self.in_features
         if workspace is None:
             workspace = torch.empty(self.workspace_size(M), dtype=torch.uint8, device=x.device)
         ro = i32_host(row_offsets)
         ns = 0 if row_offsets is None else len(row_offsets) - 1
         yd = CX_F16 if y.dtype == torch.float16 else CX_F32
-        check("cx_exl3_linear", lib().cx_exl3_linear(ctypes.byref(self.struct), ptr(x), M, ro, ns, ptr(y), yd,
-                                                     ptr(workspace), workspace.numel(), stream_ptr(stream)))
+        check("cx_exl3_linear", lib().cx_exl3_linear(ctypes.byref(self.struct), ptr(x), _xdtype(x), x.stride(0), M,
+                                                     ro, ns, ptr(y), yd, ptr(workspace), workspace.numel(),
+                                                     stream_ptr(stream)))
         return y
 
 
@@ -135,14 +141,16 @@ def route(logits: torch.Tensor, E: int, topk: int, shared_logit: torch.Tensor | 
     return sel, wts
 
 
-def group(sel: torch.Tensor, E: int, stream=None):
+def group(sel: torch.Tensor, E: int, workspace=None, stream=None):
     M, topk = sel.shape
     dev = sel.device
     counts = torch.empty(E, dtype=torch.int32, device=dev)
     offsets = torch.empty(E + 1, dtype=torch.int32, device=dev)
     pairs = torch.empty(M * topk, dtype=torch.int32, device=dev)
     rows = torch.empty(M * topk, dtype=torch.int32, device=dev)
-    ws = torch.empty(max(1, int(lib().cx_moe_group_workspace_size(M, E, topk))), dtype=torch.uint8, device=dev)
+    ws = workspace
+    if ws is None:
+        ws = torch.empty(max(1, int(lib().cx_moe_group_workspace_size(M, E, topk))), dtype=torch.uint8, device=dev)
     check("cx_moe_group", lib().cx_moe_group(ptr(sel), M, E, topk, ptr(counts), ptr(offsets), ptr(pairs), ptr(rows),
                                              ptr(ws), ws.numel(), stream_ptr(stream)))
     return counts, offsets, pairs, rows
@@ -180,7 +188,7 @@ class MoePlan:
     def __call__(self, x: torch.Tensor, logits: torch.Tensor, shared_logit: torch.Tensor | None = None,
                  row_offsets=None, mode: int = CX_MOE_AUTO, workspace=None, y=None, sel=None, wts=None, stream=None):
         M = x.shape[0]
-        assert x.dtype == torch.float16 and x.is_contiguous() and x.shape[1] == self.hidden
+        assert x.dtype in (torch.float16, torch.float32) and x.stride(1) == 1 and x.shape[1] >= self.hidden
         assert logits.dtype == torch.float32 and logits.is_contiguous()
         if y is None:
             y = torch.empty(M, self.hidden, dtype=torch.float32, device=x.device)
@@ -189,7 +197,8 @@ class MoePlan:
         ro = i32_host(row_offsets)
         ns = 0 if row_offsets is None else len(row_offsets) - 1
         check("cx_moe_layer_forward", lib().cx_moe_layer_forward(
-            self.handle, ptr(x), ptr(logits), logits.shape[1], ptr(shared_logit), M, ro, ns, ptr(y), ptr(sel),
+            self.handle, ptr(x), _xdtype(x), x.stride(0), ptr(logits), logits.shape[1], ptr(shared_logit), M, ro,
+            ns, ptr(y), ptr(sel),
             ptr(wts), mode, ptr(workspace), workspace.numel(), stream_ptr(stream)))
         return y
 
@@ -199,7 +208,7 @@ class MoePlan:
         """The layer with the residual write-back: H[r, s, :] += post[r, s] * y[r, :] for
         H of shape [M, n_streams, hidden] (or [M, ldh] with ldh >= n_streams * hidden)."""
         M = x.shape[0]
-        assert x.dtype == torch.float16 and x.is_contiguous() and x.shape[1] == self.hidden
+        assert x.dtype in (torch.float16, torch.float32) and x.stride(1) == 1 and x.shape[1] >= self.hidden
         assert logits.dtype == torch.float32 and logits.is_contiguous()
         assert post.dtype == torch.float32 and post.is_contiguous() and post.shape[0] == M
         assert H.dtype == torch.float32 and H.shape[0] == M and H.stride(-1) == 1
@@ -210,6 +219,7 @@ class MoePlan:
         ro = i32_host(row_offsets)
         ns = 0 if row_offsets is None else len(row_offsets) - 1
         check("cx_moe_layer_forward_hc", lib().cx_moe_layer_forward_hc(
-            self.handle, ptr(x), ptr(logits), logits.shape[1], ptr(shared_logit), M, ro, ns, ptr(post), n_streams,
+            self.handle, ptr(x), _xdtype(x), x.stride(0), ptr(logits), logits.shape[1], ptr(shared_logit), M, ro, ns,
+            ptr(post), n_streams,
             ptr(H), ldh, ptr(sel), ptr(wts), mode, ptr(workspace), workspace.numel(), stream_ptr(stream)))
         return H

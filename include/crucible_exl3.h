@@ -92,14 +92,17 @@ int cx_exl3_output_transform(const cx_exl3_matrix* m, const float* y_raw, int32_
 /* y = EXL3 linear of M packed activation rows.  Replaces `Build` + `RunGroup`
  * (engine/engine.hip:1046, 1731) over one `LinJob` with R = M rows, i.e. LinInKernel
  * -> split-K GEMV -> LinOutKernel (engine/exl3/exl3.h:48-82, 330-389).
- *   x         fp16 [M][in_features]
+ *   x         x_dtype CX_F16 or CX_F32, [M][ldx], ldx >= in_features, ldx % 8 == 0; fp32 rows
+ *             are rounded to fp16 inside the input transform (LinInLane's RoundH of the
+ *             engine's fp32 `src`, engine/exl3/exl3.h:60-64), no separate conversion pass
  *   row_offsets  host, nullable: n_sessions + 1 exclusive prefix sums of the rows each
  *             session packed (ragged verify spans); checked, must end at M
  *   y_dtype   CX_F32: y_h kept fp32 through the output transform (engine LinOutBlock);
  *             CX_F16: y_h rounded to fp16 before it (ref/exl3_ref.py:175 default)
  *   workspace device scratch of cx_exl3_linear_workspace_size(m, M) bytes */
 size_t cx_exl3_linear_workspace_size(const cx_exl3_matrix* m, int32_t M);
-int cx_exl3_linear(const cx_exl3_matrix* m, const uint16_t* x, int32_t M, const int32_t* row_offsets,
+int cx_exl3_linear(const cx_exl3_matrix* m, const void* x, int32_t x_dtype, int32_t ldx, int32_t M,
+                   const int32_t* row_offsets,
                    int32_t n_sessions, void* y, int32_t y_dtype, void* workspace, size_t workspace_bytes,
                    cx_stream_t stream);
 
@@ -116,7 +119,11 @@ int cx_moe_route(const float* logits, int32_t ld, int32_t M, int32_t E, int32_t 
 
 /* Stable expert-major grouping with on-device prefix sums (no host round trip).
  * counts [E], exclusive offsets [E+1], pairs [M*topk] (row * topk + slot, stable by
- * route index), row_ids [M*topk] (pairs / topk).  Replaces the MoeDispatch kernels
+ * route index), row_ids [M*topk] (pairs / topk).  sel values must lie in [0, E): the
+ * kernels check every id before using it, and a route with an id outside that range is
+ * dropped (not counted, given no position), so offsets[E] < M * topk reports it and the
+ * entries of pairs / row_ids from offsets[E] on are not written.  cx_moe_route never
+ * produces such ids; the reference traps on them (engine/layers/moe_rows.h:31, 35).  Replaces the MoeDispatch kernels
  * (engine/layers/kernels/prefill_moe.h:9-100); oracle ref/prefill_ref.py:37-45. */
 size_t cx_moe_group_workspace_size(int32_t M, int32_t E, int32_t topk);
 int cx_moe_group(const int32_t* sel, int32_t M, int32_t E, int32_t topk, int32_t* counts, int32_t* offsets,
@@ -185,24 +192,30 @@ void cx_moe_plan_destroy(cx_moe_plan* plan);
  * weighted combine (routed slots in selection order, shared expert last, fp32).
  * Replaces Engine::BlockMoe (engine/engine.hip:1327-1342, decode) and the MoE half of
  * Engine::PrefillBlock (engine/runtime/prefill_engine.inc:365-435, prefill).
- *   x             fp16 [M][H] hidden states
+ *   x             hidden states [M][ldx] of x_dtype: CX_F32 (the engine's fp32 residual-mixed
+ *                 x_, engine/engine.hip:1332; each value is rounded to fp16 inside the input
+ *                 transform as MoeRowsInSlotsKernel does, engine/layers/moe_rows.h:118-121)
+ *                 or CX_F16; ldx >= H, ldx % 8 == 0
  *   logits        fp32 [M][ld] router logits (see cx_moe_route for shared_logit)
  *   row_offsets   host, nullable: session prefix sums, checked, must end at M
  *   y             fp32 [M][H]
  *   sel, wts      nullable outputs: int32 [M][topk] and fp32 [M][topk + 1]
  *   mode          CX_MOE_DECODE / PREFILL / AUTO (by M) */
 size_t cx_moe_layer_workspace_size(const cx_moe_plan* plan, int32_t M, int32_t mode);
-int cx_moe_layer_forward(const cx_moe_plan* plan, const uint16_t* x, const float* logits, int32_t ld,
+int cx_moe_layer_forward(const cx_moe_plan* plan, const void* x, int32_t x_dtype, int32_t ldx, const float* logits,
+                         int32_t ld,
                  const float* shared_logit, int32_t M, const int32_t* row_offsets, int32_t n_sessions, float* y,
                  int32_t* sel, float* wts, int32_t mode, void* workspace, size_t workspace_bytes, cx_stream_t stream);
 
 /* The same layer with the reference's residual write-back in place of storing y:
  * H[r][s][c] += post[r][s] * y[r][c] for the n_streams hyper-connection streams of row r
  * (H row r at H + r * ldh, stream s at + s * H-width; ldh >= n_streams * hidden), fp32.
+ * H is read and written in 16-byte pieces: H must be 16-byte aligned and ldh % 4 == 0.
  * Replaces the combine's write-back in MoeRowsCombineKernel (engine/layers/moe_rows.h:
  * 672-681) and PrefillMoeCombineKernel (engine/layers/prefill_moe.h:670-679).
  *   post          fp32 [M][n_streams] */
-int cx_moe_layer_forward_hc(const cx_moe_plan* plan, const uint16_t* x, const float* logits, int32_t ld,
+int cx_moe_layer_forward_hc(const cx_moe_plan* plan, const void* x, int32_t x_dtype, int32_t ldx,
+                            const float* logits, int32_t ld,
                             const float* shared_logit, int32_t M, const int32_t* row_offsets, int32_t n_sessions,
                             const float* post, int32_t n_streams, float* H, int64_t ldh, int32_t* sel, float* wts,
                             int32_t mode, void* workspace, size_t workspace_bytes, cx_stream_t stream);

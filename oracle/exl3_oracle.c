@@ -291,7 +291,11 @@ void or_matvec(const uint16_t* x, long M, const uint16_t* w, const uint16_t* suh
 /* Top-k of E fp32 logits per row (logit descending, lower expert id on ties) and
  * the selection softmax w_k = exp(l_k - l_0) / sum_j exp(l_j - l_0) summed in rank
  * order; wts[k] = sigmoid(shared logit).  engine/layers/ops.h:683-713,
- * ref/oracle.py:227-230, docs/FLASHNEXT_FORWARD.md:238,250. */
+ * ref/oracle.py:227-230, docs/FLASHNEXT_FORWARD.md:238,250.
+ * Non-finite logits: a NaN ranks and weighs as -inf (the reference's rank count leaves
+ * NaN undefined: it flags it in a debug build, engine/layers/ops.h:691-693); +-inf rank as
+ * themselves, so a +inf top logit gives NaN weights, as exp(inf - inf) does there. */
+static double or_route_key(float v) { return v != v ? -INFINITY : (double)v; }
 void or_route(const float* logits, long ld, long M, int E, int topk, const float* shared_logit,
               int32_t* sel, float* wts) {
 #pragma omp parallel for schedule(static)
@@ -304,14 +308,15 @@ void or_route(const float* logits, long ld, long M, int E, int topk, const float
         int taken = 0;
         for (int j = 0; j < k; ++j) taken |= s[j] == e;
         if (taken) continue;
-        if (best < 0 || lg[e] > lg[best]) best = e; /* strict: lower id wins ties */
+        if (best < 0 || or_route_key(lg[e]) > or_route_key(lg[best])) best = e; /* strict: lower id wins ties */
       }
       s[k] = best;
     }
+    const double top = or_route_key(lg[s[0]]);
     double sum = 0.0;
-    for (int k = 0; k < topk; ++k) sum += exp((double)lg[s[k]] - (double)lg[s[0]]);
+    for (int k = 0; k < topk; ++k) sum += exp(or_route_key(lg[s[k]]) - top);
     float* w = wts + r * (topk + 1);
-    for (int k = 0; k < topk; ++k) w[k] = (float)(exp((double)lg[s[k]] - (double)lg[s[0]]) / sum);
+    for (int k = 0; k < topk; ++k) w[k] = (float)(exp(or_route_key(lg[s[k]]) - top) / sum);
     const double sl = shared_logit ? shared_logit[r] : lg[E];
     w[topk] = (float)(1.0 / (1.0 + exp(-sl)));
   }

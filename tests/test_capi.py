@@ -55,5 +55,13 @@ def test_argument_errors_without_gpu():
     assert L.cx_exl3_output_transform(ctypes.byref(m), ctypes.c_void_p(1), 2, ctypes.c_void_p(1), 5, None) == -1
     # rows must match the session offsets
     ro = exl3moe.i32_host([0, 2, 5])
-    assert L.cx_exl3_linear(ctypes.byref(m), ctypes.c_void_p(1), 4, ro, 2, ctypes.c_void_p(1), 1,
-                            ctypes.c_void_p(1), 1 << 30, None) == -2
+    assert L.cx_exl3_linear(ctypes.byref(m), ctypes.c_void_p(256), 0, 2048, 4, ro, 2, ctypes.c_void_p(256), 1,
+                            ctypes.c_void_p(256), 1 << 30, None) == -2
+    # activation dtype, row stride and alignment are checked before any launch
+    ro = exl3moe.i32_host([0, 2, 4])
+    assert L.cx_exl3_linear(ctypes.byref(m), ctypes.c_void_p(256), 3, 2048, 4, ro, 2, ctypes.c_void_p(256), 1,
+                            ctypes.c_void_p(256), 1 << 30, None) == -1
+    assert L.cx_exl3_linear(ctypes.byref(m), ctypes.c_void_p(256), 1, 2044, 4, ro, 2, ctypes.c_void_p(256), 1,
+                            ctypes.c_void_p(256), 1 << 30, None) == -2
+    assert L.cx_exl3_linear(ctypes.byref(m), ctypes.c_void_p(258), 0, 2048, 4, ro, 2, ctypes.c_void_p(256), 1,
+                            ctypes.c_void_p(256), 1 << 30, None) == -2

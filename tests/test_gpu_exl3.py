@@ -86,6 +86,27 @@ def test_config2_ragged_gemv(ops, I, O_):
     assert np.abs(y - ref).max() <= 1e-3 * np.abs(ref).max()
 
 
+@pytest.mark.parametrize("I,O_", [(2048, 4096), (4096, 2048)])
+def test_config2_fp32_input(ops, I, O_):
+    # fp32 activations (LinJob.src, engine/exl3/exl3.h:20-33) in a strided buffer: bitwise
+    # the fp16 path on x rounded to fp16, and within tolerance of the oracle.
+    from exl3moe import synth
+    rng = np.random.default_rng(12 + I)
+    tr, suh, svh = synth.linear(rng, I, O_, 4)
+    lin = ops.DeviceLinear.from_trellis(tr, suh, svh, 4)
+    offs = synth.sessions(rng, 8, 1, 5)
+    M = offs[-1]
+    xf = (rng.standard_normal((M, I)) * 2.3).astype(np.float32)
+    buf = torch.zeros(M, I + 40, dtype=torch.float32, device="cuda")
+    buf[:, :I] = torch.from_numpy(xf).cuda()
+    y32 = lin(buf[:, :I], torch.float32, row_offsets=offs).cpu().numpy()
+    xh = xf.astype(np.float16)
+    y16 = lin(torch.from_numpy(xh).cuda(), torch.float32, row_offsets=offs).cpu().numpy()
+    np.testing.assert_array_equal(y32.view(np.uint32), y16.view(np.uint32))
+    ref = O.matvec(xh, O.reconstruct_inner(tr, 4), suh, svh, np.float32)
+    assert rel_l2(y32, ref) <= 1e-3
+
+
 @pytest.mark.parametrize("bits", [1.5, 2.5, 3, 5, 6, 7, 8])
 def test_linear_other_rates(ops, bits):
     from exl3moe import synth

@@ -220,27 +220,56 @@ def test_config4_prefill_subset(ops, layer512):
 
 @pytest.mark.parametrize("mode", [1, 2])
 def test_hc_writeback(ops, mode):
-    # H[r, s] += post[r, s] * y[r] over 4 streams, in a strided H (ldh > 4 * hidden);
-    # y from the plain forward on the same inputs (the layer computation is shared, so y
-    # is bitwise the same; the write-back is one fp32 multiply-add per element).
+    # H[r, s] += post[r, s] * y[r] over 4 streams, in a strided H (ldh > 4 * hidden), checked
+    # against the oracle's layer output on the same routing (engine/layers/moe_rows.h:672-681).
     from exl3moe import synth
     plan = synth.device_moe_layer(13, E=16, H=256, Ie=128, topk=4)
     rng = np.random.default_rng(3)
     M, S, ldh = 37, 4, 4 * 256 + 64
-    x = torch.from_numpy(rng.standard_normal((M, 256)).astype(np.float16)).cuda()
-    lg = torch.from_numpy(rng.standard_normal((M, 17)).astype(np.float32)).cuda()
-    post = torch.from_numpy(rng.standard_normal((M, S)).astype(np.float32)).cuda()
+    xh = rng.standard_normal((M, 256)).astype(np.float16)
+    lgh = rng.standard_normal((M, 17)).astype(np.float32)
+    x = torch.from_numpy(xh).cuda()
+    lg = torch.from_numpy(lgh).cuda()
+    p = rng.standard_normal((M, S)).astype(np.float32)
+    post = torch.from_numpy(p).cuda()
     H0 = rng.standard_normal((M, ldh)).astype(np.float32)
     Hd = torch.from_numpy(H0.copy()).cuda()
-    y = plan(x, lg, mode=mode).cpu().numpy()
-    plan.forward_hc(x, lg, post, Hd, mode=mode)
+    sel = torch.empty(M, 4, dtype=torch.int32, device="cuda")
+    wts = torch.empty(M, 5, dtype=torch.float32, device="cuda")
+    plan.forward_hc(x, lg, post, Hd, mode=mode, sel=sel, wts=wts)
     got = Hd.cpu().numpy()
+    rs, rw = O.route(lgh, 16, 4)
+    np.testing.assert_array_equal(sel.cpu().numpy(), rs)
+    ref = oracle_layer(plan, xh, rs, rw)
+    for s in range(S):
+        delta = got[:, s * 256:(s + 1) * 256].astype(np.float64) - H0[:, s * 256:(s + 1) * 256]
+        want = p[:, s:s + 1].astype(np.float64) * ref
+        assert rel_l2(delta, want) <= 1e-3, s
+    np.testing.assert_array_equal(got[:, S * 256:], H0[:, S * 256:])  # padding untouched
+    # The write-back is one fp32 multiply-add per element on the plain forward's y.
+    y = plan(x, lg, mode=mode).cpu().numpy()
     exp = H0.copy()
-    p = post.cpu().numpy()
     for s in range(S):
         exp[:, s * 256:(s + 1) * 256] += p[:, s:s + 1] * y
     np.testing.assert_allclose(got, exp, rtol=0, atol=1e-5 * float(np.abs(exp).max()))
-    np.testing.assert_array_equal(got[:, S * 256:], H0[:, S * 256:])  # padding untouched
+
+
+def test_hc_writeback_config3(ops, layer512):
+    # The config-3 shape (E = 512, H = 2048, 24 decode rows) with 2 streams, against the oracle.
+    rng = np.random.default_rng(31)
+    M, S = 24, 2
+    xh = rng.standard_normal((M, 2048)).astype(np.float16)
+    lgh = rng.standard_normal((M, 513)).astype(np.float32)
+    p = rng.standard_normal((M, S)).astype(np.float32)
+    H0 = rng.standard_normal((M, S * 2048)).astype(np.float32)
+    Hd = torch.from_numpy(H0.copy()).cuda()
+    layer512.forward_hc(torch.from_numpy(xh).cuda(), torch.from_numpy(lgh).cuda(), torch.from_numpy(p).cuda(), Hd,
+                        mode=1)
+    got = Hd.cpu().numpy().astype(np.float64)
+    rs, rw = O.route(lgh, 512, 10)
+    ref = oracle_layer(layer512, xh, rs, rw)
+    for s in range(S):
+        assert rel_l2(got[:, s * 2048:(s + 1) * 2048] - H0[:, s * 2048:(s + 1) * 2048], p[:, s:s + 1] * ref) <= 1e-3
 
 
 def test_hc_errors(ops):
@@ -251,6 +280,12 @@ def test_hc_errors(ops):
     post = torch.zeros(2, 4, dtype=torch.float32, device="cuda")
     with pytest.raises(CxError) as e:
         plan.forward_hc(x, lg, post, torch.zeros(2, 3 * 256, device="cuda"))  # ldh < 4 * hidden
+    assert e.value.rc == -2
+    with pytest.raises(CxError) as e:  # ldh not a multiple of 4 (16-byte rows)
+        plan.forward_hc(x, lg, post, torch.zeros(2, 4 * 256 + 2, device="cuda"))
+    assert e.value.rc == -2
+    with pytest.raises(CxError) as e:  # H not 16-byte aligned
+        plan.forward_hc(x, lg, post, torch.zeros(2, 4 * 256 + 5, device="cuda")[:, 1:])
     assert e.value.rc == -2
 
 
@@ -308,3 +343,107 @@ def test_many_experts_layer(ops, mode):
         e = rel_l2(y, ref)
         print(f"E=600 k=16 mode={mode} M={M} rel_l2={e:.3e}")
         assert e <= 1e-3
+
+
+def test_route_nonfinite(ops):
+    # NaN ranks and weighs as -inf, +-inf rank as themselves, ids break ties (the oracle's
+    # documented order; the reference leaves NaN undefined).
+    rng = np.random.default_rng(9)
+    for E, k in [(64, 10), (512, 10), (1000, 16)]:
+        M = 12
+        lg = rng.standard_normal((M, E + 1)).astype(np.float32)
+        lg[0, [3, 17, 40]] = np.nan
+        lg[1, :] = np.nan
+        lg[2, [8, 2]] = np.inf
+        lg[3, ::2] = -np.inf
+        lg[4, :E - 3] = -np.inf
+        lg[5, [1, 5]] = [np.nan, -np.inf]
+        lg[6, :] = -np.inf
+        lg[7, rng.permutation(E)[:E // 2]] = np.nan
+        sel, wts = ops.route(torch.from_numpy(lg).cuda(), E, k)
+        rs, rw = O.route(lg, E, k)
+        np.testing.assert_array_equal(sel.cpu().numpy(), rs)
+        np.testing.assert_allclose(wts.cpu().numpy(), rw, rtol=2e-6, atol=1e-7, equal_nan=True)
+
+
+@pytest.mark.parametrize("M", [7, 300])
+def test_group_drops_out_of_range_ids(ops, M):
+    # Ids outside [0, E) are dropped: not counted, no position (offsets[E] < M k shows it);
+    # the valid routes keep their stable expert-major order.  Both grouping paths (one
+    # workgroup up to 2048 routes, tiled above).
+    rng = np.random.default_rng(M)
+    E, k = 64, 10
+    sel = rng.integers(0, E, size=(M, k)).astype(np.int32)
+    bad = rng.random((M, k)) < 0.1
+    sel[bad] = rng.choice(np.array([-1, E, E + 7, 1 << 30, -(1 << 31)], dtype=np.int64), size=int(bad.sum()))
+    valid = ~bad
+    counts, offsets, pairs, rows = [t.cpu().numpy() for t in ops.group(torch.from_numpy(sel).cuda(), E)]
+    want_counts = np.bincount(sel[valid], minlength=E)
+    np.testing.assert_array_equal(counts, want_counts)
+    np.testing.assert_array_equal(offsets, np.concatenate([[0], np.cumsum(want_counts)]))
+    flat = sel.ravel()
+    idx = np.nonzero(valid.ravel())[0]
+    want_pairs = idx[np.argsort(flat[idx], kind="stable")]
+    n = int(offsets[E])
+    assert n == int(valid.sum()) < M * k
+    np.testing.assert_array_equal(pairs[:n], want_pairs)
+    np.testing.assert_array_equal(rows[:n], want_pairs // k)
+
+
+def _poison(ws):
+    ws.fill_(0xFF)  # every float in the scratch is a NaN, every int is -1
+    return ws
+
+
+@pytest.mark.parametrize("mode", [1, 2])
+def test_workspace_poisoning(ops, layer512, mode):
+    # The reference fills scratch with NaN in a debug build (engine/exl3/plans.h:48-62): no
+    # output may depend on what the workspace held before the call.
+    rng = np.random.default_rng(77)
+    M = 24 if mode == 1 else 300
+    x = torch.from_numpy(rng.standard_normal((M, 2048)).astype(np.float16)).cuda()
+    lg = torch.from_numpy(rng.standard_normal((M, 513)).astype(np.float32)).cuda()
+    n = layer512.workspace_size(M, mode)
+    clean = layer512(x, lg, mode=mode, workspace=torch.zeros(n, dtype=torch.uint8, device="cuda"))
+    for _ in range(2):
+        got = layer512(x, lg, mode=mode, workspace=_poison(torch.empty(n, dtype=torch.uint8, device="cuda")))
+        assert torch.equal(got.view(torch.int32), clean.view(torch.int32))
+
+
+def test_workspace_poisoning_linear_group(ops):
+    from exl3moe import synth
+    rng = np.random.default_rng(78)
+    tr, suh, svh = synth.linear(rng, 2048, 4096, 4)
+    lin = ops.DeviceLinear.from_trellis(tr, suh, svh, 4)
+    for M in (1, 24, 130):
+        x = torch.from_numpy(rng.standard_normal((M, 2048)).astype(np.float16)).cuda()
+        n = lin.workspace_size(M)
+        clean = lin(x, workspace=torch.zeros(n, dtype=torch.uint8, device="cuda"))
+        got = lin(x, workspace=_poison(torch.empty(n, dtype=torch.uint8, device="cuda")))
+        assert torch.equal(got.view(torch.int32), clean.view(torch.int32))
+    sel = torch.from_numpy(rng.integers(0, 512, size=(3000, 10)).astype(np.int32)).cuda()
+    want = ops.group(sel, 512)
+    got = ops.group(sel, 512, workspace=_poison(torch.empty(1 << 20, dtype=torch.uint8, device="cuda")))
+    for a, b in zip(want, got):
+        assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("mode", [1, 2])
+def test_fp32_input(ops, layer512, mode):
+    # fp32 hidden states (the engine's x_) in a strided buffer: bitwise the fp16 path on
+    # x rounded to fp16, and within tolerance of the oracle.
+    rng = np.random.default_rng(90 + mode)
+    M = 24 if mode == 1 else 200
+    xf = (rng.standard_normal((M, 2048)) * 0.7).astype(np.float32)  # not an fp16 grid
+    lgh = rng.standard_normal((M, 513)).astype(np.float32)
+    lg = torch.from_numpy(lgh).cuda()
+    buf = torch.zeros(M, 2048 + 64, dtype=torch.float32, device="cuda")
+    buf[:, :2048] = torch.from_numpy(xf).cuda()
+    y32 = layer512(buf[:, :2048], lg, mode=mode).cpu().numpy()
+    xh = xf.astype(np.float16)
+    y16 = layer512(torch.from_numpy(xh).cuda(), lg, mode=mode).cpu().numpy()
+    np.testing.assert_array_equal(y32.view(np.uint32), y16.view(np.uint32))
+    rows = np.arange(M) if mode == 1 else np.sort(rng.choice(M, size=24, replace=False))
+    rs, rw = O.route(lgh, 512, 10)
+    ref = oracle_layer(layer512, xh[rows], rs[rows], rw[rows])
+    assert rel_l2(y32[rows], ref) <= 1e-3

@@ -93,6 +93,29 @@ def test_route_against_sort():
     np.testing.assert_allclose(w2[:, k], 1 / (1 + np.exp(-shared.astype(np.float64))), rtol=1e-6)
 
 
+def test_route_nonfinite_against_sort():
+    # NaN ranks and weighs as -inf; +-inf rank as themselves (ids break ties).
+    rng = np.random.default_rng(9)
+    M, E, k = 12, 64, 10
+    logits = rng.standard_normal((M, E + 1)).astype(np.float32)
+    logits[0, [3, 17, 40]] = np.nan
+    logits[1, :] = np.nan
+    logits[2, [8, 2]] = np.inf
+    logits[3, ::2] = -np.inf
+    logits[4, :E - 3] = -np.inf
+    logits[5, [1, 5]] = [np.nan, -np.inf]
+    sel, wts = O.route(logits, E, k)
+    key = np.where(np.isnan(logits), -np.inf, logits).astype(np.float64)
+    for r in range(M):
+        order = sorted(range(E), key=lambda e: (-key[r, e], e))[:k]
+        assert sel[r].tolist() == order, r
+        with np.errstate(invalid="ignore"):
+            w = np.exp(key[r, order] - key[r, order[0]])
+            np.testing.assert_allclose(wts[r, :k], w / w.sum(), rtol=1e-6)
+    assert sel[2, :2].tolist() == [2, 8] and np.isnan(wts[2, :k]).all()
+    assert sel[1].tolist() == list(range(k))  # all NaN: ids in order
+
+
 def test_dispatch_known_answer():
     # ref/test_prefill.py:31-38
     counts, offsets, pairs, rows = O.dispatch(np.array([[2, 1, 0], [0, 2, 1], [1, 0, 2]]), 4)
