@@ -8,6 +8,7 @@
 // rows [M k, M k + M) are the shared expert's rows 0..M-1.  Every expert's rows are
 // contiguous, so an expert GEMM reads one contiguous block of activation rows.
 #include <cstdlib>
+#include <mutex>
 #include <new>
 
 #include "internal.hpp"
@@ -577,6 +578,7 @@ struct cx_moe_plan {
   cx::ExpertTables tb;
   hipEvent_t* trace;                 // caller's events (nullable), recorded between stages
   int n_trace, trace_cursor;
+  void* scratch;                     // this device's address of the library's static scratch
 };
 
 namespace cx {
@@ -649,6 +651,36 @@ MoeSizes PlanMoe(const cx_moe_plan* pl, int M, int mode) {
   s.off_yd = take((size_t)s.P * pl->H * 4);
   s.total = o;
   return s;
+}
+
+// ---- the allocation-free variant's scratch --------------------------------------------
+// One static device array per GPU, used as the workspace of cx_moe_layer_forward_static.
+// Host code never uses the array's name as an address (on the host it is a stand-in):
+// its device address is looked up once per device, with that device current, when the
+// first plan is created there, and kept in g_scratch[device] and in every plan.
+static __device__ __align__(256) unsigned char scratch[CX_STATIC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch[kMaxDevices];
+
+// Device address of `scratch` on the current device (nullptr with *err set on failure).
+void* StaticScratch(hipError_t* err) {
+  int dev = 0;
+  *err = hipGetDevice(&dev);
+  if (*err != hipSuccess) return nullptr;
+  if (dev < 0 || dev >= kMaxDevices) {
+    *err = hipErrorInvalidDevice;
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* p = nullptr;
+    *err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (*err != hipSuccess) return nullptr;
+    g_scratch[dev] = p;
+  }
+  return g_scratch[dev];
 }
 
 void LaunchRoute(const float* logits, int ld, int M, int E, int topk, const float* shared_logit, int* sel, float* wts,
@@ -847,6 +879,13 @@ int cx_moe_plan_create(const cx_moe_layer* layer, cx_moe_plan** out) {
     return (int)err;
   }
   pl->tb = ExpertTables{pl->d_tables, pl->d_tables + n, pl->d_tables + 2 * n, g_suh, u_suh, g_svh, u_svh, d_suh};
+  pl->scratch = StaticScratch(&err);
+  if (err != hipSuccess) {
+    (void)hipFree(pl->d_scales);
+    (void)hipFree(pl->d_tables);
+    delete pl;
+    return (int)err;
+  }
   *out = pl;
   return CX_OK;
 }
@@ -978,6 +1017,19 @@ int cx_moe_layer_forward_hc(const cx_moe_plan* pl, const void* x, int32_t x_dtyp
   const HcArgs hc{post, H, (long long)ldh, n_streams};
   return MoeForward(pl, x, x_dtype, ldx, logits, ld, shared_logit, M, row_offsets, n_sessions, nullptr, &hc, sel, wts, mode,
                     workspace, workspace_bytes, stream);
+}
+
+int cx_moe_layer_forward_static(const cx_moe_plan* pl, const void* x, int32_t x_dtype, int32_t ldx,
+                                const float* logits, int32_t ld, const float* shared_logit, int32_t M,
+                                const int32_t* row_offsets, int32_t n_sessions, float* y, int32_t* sel, float* wts,
+                                int32_t mode, cx_stream_t stream) {
+  if (!pl || !y) return CX_E_ARG;
+  if (!pl->scratch) return CX_E_ARG;
+  if (M <= 0) return CX_E_SHAPE;
+  // The whole workspace lives in the static array; nothing is allocated here.
+  if (PlanMoe(pl, M, mode).total > (size_t)CX_STATIC_SCRATCH_BYTES) return CX_E_WORKSPACE;
+  return MoeForward(pl, x, x_dtype, ldx, logits, ld, shared_logit, M, row_offsets, n_sessions, y, nullptr, sel, wts,
+                    mode, pl->scratch, (size_t)CX_STATIC_SCRATCH_BYTES, stream);
 }
 
 int cx_moe_plan_set_trace(cx_moe_plan* plan, void* const* events, int32_t n_events) {

@@ -24,7 +24,7 @@ EXPORTED = [
     "cx_exl3_output_transform", "cx_exl3_linear_workspace_size", "cx_exl3_linear",
     "cx_exl3_group_workspace_size", "cx_exl3_group",
     "cx_dense_linear", "cx_moe_route", "cx_moe_group_workspace_size", "cx_moe_group", "cx_moe_plan_create", "cx_moe_plan_destroy",
-    "cx_moe_layer_workspace_size", "cx_moe_layer_forward", "cx_moe_layer_forward_hc", "cx_moe_plan_set_trace",
+    "cx_moe_layer_workspace_size", "cx_moe_layer_forward", "cx_moe_layer_forward_hc", "cx_moe_layer_forward_static", "cx_moe_plan_set_trace",
     "cx_checkpoint_open", "cx_checkpoint_close", "cx_checkpoint_count", "cx_checkpoint_name", "cx_checkpoint_tensor",
     "cx_exl3_linear_info", "cx_exl3_load_linear", "cx_last_error", "cx_version",
 ]

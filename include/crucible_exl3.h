@@ -207,6 +207,22 @@ int cx_moe_layer_forward(const cx_moe_plan* plan, const void* x, int32_t x_dtype
                  const float* shared_logit, int32_t M, const int32_t* row_offsets, int32_t n_sessions, float* y,
                  int32_t* sel, float* wts, int32_t mode, void* workspace, size_t workspace_bytes, cx_stream_t stream);
 
+/* The layer without a workspace argument, for callers that cannot allocate (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  No
+ * counterpart in the reference.  The workspace is a static device array of
+ * CX_STATIC_SCRATCH_BYTES inside the library (one per GPU, held until the process ends;
+ * its address is looked up when the first plan is created on that GPU); the call
+ * allocates nothing.  Returns CX_E_WORKSPACE when cx_moe_layer_workspace_size(plan, M,
+ * mode) exceeds CX_STATIC_SCRATCH_BYTES (at H = 2048, I = 512, top-10: decode calls up to
+ * M = 64 rows fit).  Every call on one GPU shares the array: calls that overlap in time on
+ * one GPU (other streams, other host threads) race and must be serialised by the caller.
+ * Nothing in the array needs to start at zero.  Arguments as for cx_moe_layer_forward. */
+#define CX_STATIC_SCRATCH_BYTES (24 << 20)
+int cx_moe_layer_forward_static(const cx_moe_plan* plan, const void* x, int32_t x_dtype, int32_t ldx,
+                                const float* logits, int32_t ld, const float* shared_logit, int32_t M,
+                                const int32_t* row_offsets, int32_t n_sessions, float* y, int32_t* sel, float* wts,
+                                int32_t mode, cx_stream_t stream);
+
 /* The same layer with the reference's residual write-back in place of storing y:
  * H[r][s][c] += post[r][s] * y[r][c] for the n_streams hyper-connection streams of row r
  * (H row r at H + r * ldh, stream s at + s * H-width; ldh >= n_streams * hidden), fp32.
