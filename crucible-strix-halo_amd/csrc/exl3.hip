@@ -208,6 +208,22 @@ bool LaunchGemmPrefill(int k2, int cb, int nrbt, int wpg, dim3 grid, const GemmA
   }
 }
 
+bool LaunchGemmTall(int k2, int cb, dim3 grid, const GemmArgs& g, hipStream_t s) {
+  switch (k2) {
+    case 2: return LaunchGemmTallRate2(cb, grid, g, s);
+    case 3: return LaunchGemmTallRate3(cb, grid, g, s);
+    case 4: return LaunchGemmTallRate4(cb, grid, g, s);
+    case 5: return LaunchGemmTallRate5(cb, grid, g, s);
+    case 6: return LaunchGemmTallRate6(cb, grid, g, s);
+    case 7: return LaunchGemmTallRate7(cb, grid, g, s);
+    case 8: return LaunchGemmTallRate8(cb, grid, g, s);
+    case 10: return LaunchGemmTallRate10(cb, grid, g, s);
+    case 12: return LaunchGemmTallRate12(cb, grid, g, s);
+    case 14: return LaunchGemmTallRate14(cb, grid, g, s);
+    case 16: return LaunchGemmTallRate16(cb, grid, g, s);
+    default: return false;
+  }
+}
 
 size_t LinearWorkspace(const LinearPlan& p, int I, int O, int M) {
   return AlignUp((size_t)M * I * 2, 256) + AlignUp((size_t)p.S * M * O * 4, 256);

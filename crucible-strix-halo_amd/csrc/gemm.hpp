@@ -21,6 +21,8 @@
 //   of 16 rows per wave, all fed by the same decoded weights.
 #pragma once
 
+#include <utility>
+
 #include "decode.hpp"
 
 
@@ -516,16 +518,11 @@ __global__ void __launch_bounds__(64 * WPG) Exl3GemmPrefillKernel(GemmArgs g) {
     __syncthreads();  // the epilogue reuses the tile buffers
   };
   using std::integral_constant;
-  if (nrb <= 1) main_loop(integral_constant<int, 1>{});
-  else if (nrb == 2) main_loop(integral_constant<int, 2>{});
-  else if (nrb == 3) main_loop(integral_constant<int, 3>{});
-  else if (nrb == 4 || NRBT == 4) main_loop(integral_constant<int, 4>{});
-  else if constexpr (NRBT == 8) {
-    if (nrb == 5) main_loop(integral_constant<int, 5>{});
-    else if (nrb == 6) main_loop(integral_constant<int, 6>{});
-    else if (nrb == 7) main_loop(integral_constant<int, 7>{});
-    else main_loop(integral_constant<int, 8>{});
-  }
+  // main_loop<NA> for NA = clamp(nrb, 1, NRBT): a chain of compile-time tests.
+  [&]<int... Is>(std::integer_sequence<int, Is...>) {
+    const int na = nrb < 1 ? 1 : nrb > NRBT ? NRBT : nrb;
+    (void)((na == Is + 1 ? (main_loop(integral_constant<int, Is + 1>{}), true) : false) || ...);
+  }(std::make_integer_sequence<int, NRBT>{});
 
   if (pl.epi == 1) {
     // Output transform per 128-column block: stage y_h rows in LDS, ER rows at a time
@@ -594,3 +591,224 @@ __global__ void __launch_bounds__(64 * WPG) Exl3GemmPrefillKernel(GemmArgs g) {
 }
 
 }  // namespace cx
+
+namespace cx {
+
+// Tall prefill GEMM for long entries: a workgroup = 4 waves owns 128 columns (4 column
+// pairs) x up to 16 NRBW row blocks of one entry, full K.  Wave w decodes column pair w
+// per step and passes its B fragments to the other waves through LDS; wave w multiplies
+// row blocks w, w + 4, ... by all 8 column tiles.  So every tile is decoded once per
+// entry of up to 64 NRBW rows, and every activation fragment is loaded by exactly one
+// wave, straight into registers (no activation staging, no sharing needed).
+//
+// Step pipeline (one workgroup barrier per step, B fragments double buffered):
+//   barrier s | read B(s) from LDS | MFMAs of step s, decode of step s + 1 | write B(s + 1)
+// The buffer written for step s + 1 was last read for step s - 1, before barrier s.
+template <int K2, int CB, int NRBW>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+Exl3GemmTallKernel(GemmArgs g) {
+  constexpr int T = TileDwords(K2);
+  constexpr int SD = 4 * T;
+  constexpr int DPL = (SD + 63) / 64;
+  constexpr int ND = WindowDwords(K2);
+  constexpr int ER = 16;                       // epilogue slab rows (one row block)
+  constexpr int BBYTES = 2 * 4 * 2 * 64 * 16;  // [buffer][column pair][fragment][lane] x 16 B
+  constexpr int EBYTES = 4 * ER * 132 * 4;     // one slab per wave
+  __shared__ uint32_t stage[4][StageDwords<DPL>()];
+  __shared__ __align__(16) char smem[BBYTES > EBYTES ? BBYTES : EBYTES];
+  u32x4_t* bs = reinterpret_cast<u32x4_t*>(smem);
+  const int n_entries = g.n_entries ? *g.n_entries : g.n_entries_host;
+  const GridPos gp = XcdEntryMajor();
+  const int ei = gp.y + g.entry_base;
+  if (ei >= n_entries) return;
+  const int4 ent = EntryOf(g, ei);
+  const GemmPlane& pl = g.plane[gp.z];
+  const int cpg = gp.x;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int steps = g.A / 2;
+  const int row0 = ent.y, nrows = ent.z;
+  if (nrows <= 0) return;
+  const int nrb = (nrows + 15) / 16;
+  const MatPtr m = MatOf(g, pl, ent.x);
+  const LaneRun<K2> lr(lane);
+  const int cp = cpg * 4 + wave;
+  const __amdgpu_buffer_rsrc_t rw = MakeRsrc(m.tiles + (size_t)cp * g.A * 2 * T, (uint32_t)steps * SD * 4);
+  uint32_t woff[2][ND];
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int i = 0; i < ND; ++i) woff[j][i] = (uint32_t)StagePad((2 * j + lr.tile) * T + (lr.d0 + i) % T);
+  const uint32_t loff = (uint32_t)lane * DPL * 4;
+  uint32_t* slot = stage[wave];
+  // Activations: rows past the entry lie outside the buffer resource and read as zeros.
+  const __amdgpu_buffer_rsrc_t rx = MakeRsrc(pl.x + (size_t)row0 * pl.ldx, (uint32_t)nrows * pl.ldx * 2);
+
+  // A step's weights go through the wave's LDS slot: staged (written) one step before its
+  // decode, windows read back at the start of the decode's step.
+  auto stage_w = [&](const Dwords<DPL>& w) { StageWrite<DPL>(slot, lane, w.v); };
+  auto read_windows = [&](uint32_t (&v)[2][3]) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+#pragma unroll
+      for (int i = 0; i < ND; ++i) v[j][i] = slot[woff[j][i]];
+      if constexpr (ND == 2) v[j][2] = 0u;
+    }
+  };
+  auto decode = [&](const uint32_t (&v)[2][3], half8_t& b0, half8_t& b1) {
+    half4_t lo0, hi0, lo1, hi1;
+    DecodeRun<K2, CB>(v[0][0], v[0][1], v[0][2], lr.shift, lo0, hi0);
+    DecodeRun<K2, CB>(v[1][0], v[1][1], v[1][2], lr.shift, lo1, hi1);
+    b0 = half8_t{lo0[0], lo0[1], lo0[2], lo0[3], lo1[0], lo1[1], lo1[2], lo1[3]};
+    b1 = half8_t{hi0[0], hi0[1], hi0[2], hi0[3], hi1[0], hi1[1], hi1[2], hi1[3]};
+  };
+  auto write_b = [&](int buf, const half8_t& b0, const half8_t& b1) {
+    bs[((buf * 4 + wave) * 2 + 0) * 64 + lane] = __builtin_bit_cast(u32x4_t, b0);
+    bs[((buf * 4 + wave) * 2 + 1) * 64 + lane] = __builtin_bit_cast(u32x4_t, b1);
+  };
+
+  auto main_loop = [&](auto nac) {
+    constexpr int NA = decltype(nac)::value;  // row blocks per wave
+    constexpr int PFW = 2;                    // weight steps in flight (beyond the staged one)
+    constexpr int PFA = 2;                    // activation steps in flight
+    uint32_t xoff[NA];
+#pragma unroll
+    for (int i = 0; i < NA; ++i)
+      xoff[i] = (uint32_t)(((wave + 4 * i) * 16 + (lane & 15)) * pl.ldx * 2 + 16 * (lane >> 4));
+    float4_t acc[NA][4][2];
+#pragma unroll
+    for (int i = 0; i < NA; ++i)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) acc[i][c][0] = acc[i][c][1] = float4_t{0.f, 0.f, 0.f, 0.f};
+    Dwords<DPL> wq[PFW];  // slot j % PFW: step j's weights until they are staged
+    u32x4_t aq[PFA][NA];
+    // Loads are unconditional, also past the last step (outside the buffer resources: no
+    // memory access, zeros), so the compiler can count the loads in flight.
+#pragma unroll
+    for (int k = 0; k < PFW; ++k) wq[k] = BufLoadN<DPL>(rw, loff, (uint32_t)k * SD * 4);
+#pragma unroll
+    for (int k = 0; k < PFA; ++k)
+#pragma unroll
+      for (int i = 0; i < NA; ++i) aq[k][i] = BufLoad128(rx, xoff[i], (uint32_t)k * 64);
+    {  // step 0 decoded and published, step 1 staged
+      stage_w(wq[0]);
+      wq[0] = BufLoadN<DPL>(rw, loff, (uint32_t)PFW * SD * 4);
+      __builtin_amdgcn_wave_barrier();
+      uint32_t v[2][3];
+      read_windows(v);
+      __builtin_amdgcn_wave_barrier();
+      half8_t b0, b1;
+      decode(v, b0, b1);
+      write_b(0, b0, b1);
+      stage_w(wq[1]);
+      wq[1] = BufLoadN<DPL>(rw, loff, (uint32_t)(PFW + 1) * SD * 4);
+    }
+    constexpr int UN = 4;  // lcm(PFW, PFA, 2): fixed queue slots and buffers per unrolled step
+    constexpr int NM = NA * 8;  // MFMAs per step
+    for (int s0 = 0; s0 < steps; s0 += UN) {
+#pragma unroll
+      for (int u = 0; u < UN; ++u) {
+        const int s = s0 + u;
+        __syncthreads();
+        half8_t bf[4][2];
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+          for (int f = 0; f < 2; ++f) bf[c][f] = __builtin_bit_cast(half8_t, bs[(((u & 1) * 4 + c) * 2 + f) * 64 + lane]);
+        uint32_t v[2][3];
+        read_windows(v);  // step s + 1, staged in the previous step
+        __builtin_amdgcn_sched_barrier(0);
+        // MFMAs of step s (column-tile major, so the first ones need only the first B
+        // fragment) interleaved with the decode of step s + 1: the matrix core and the
+        // VALU work side by side within the wave.
+        half8_t n0, n1;
+        decode(v, n0, n1);
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+          for (int f = 0; f < 2; ++f)
+#pragma unroll
+            for (int i = 0; i < NA; ++i)
+              acc[i][c][f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, aq[u % PFA][i]),
+                                                                    bf[c][f], acc[i][c][f], 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < NA; ++i) {
+          aq[u % PFA][i] = BufLoad128(rx, xoff[i], (uint32_t)(s + PFA) * 64);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+#pragma unroll
+        for (int k = 0; k < NM - 2; ++k) {
+          __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        write_b((u + 1) & 1, n0, n1);  // step s + 1 (past the last step: never read)
+        stage_w(wq[u % PFW]);          // step s + 2
+        wq[u % PFW] = BufLoadN<DPL>(rw, loff, (uint32_t)(s + 2 + PFW) * SD * 4);
+      }
+    }
+    __syncthreads();  // every wave is done with the B buffers: the epilogue reuses them
+
+    if (pl.epi == 1) {
+      // Output transform per row: the wave holds all 128 columns of its row blocks.
+      // Stage one row block (16 x 128 fp32) in the wave's slab, then WHT128 * norm * svh.
+      float(*eb)[132] = reinterpret_cast<float(*)[132]>(smem + wave * ER * 132 * 4);
+      const int j = lane & 15;
+      const int c0 = cpg * 128 + 8 * j;
+      float sv[8];
+      LoadH8(m.svh + c0, sv);
+#pragma unroll
+      for (int i = 0; i < NA; ++i) {
+        const int rb = wave + 4 * i;
+        if (rb >= nrb) break;  // wave-uniform
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int cl = c * 32 + ((lane & 15) >> 3) * 16 + (lane & 7);
+            eb[4 * (lane >> 4) + e][cl] = acc[i][c][0][e];
+            eb[4 * (lane >> 4) + e][cl + 8] = acc[i][c][1][e];
+          }
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int rr = 4 * q + (lane >> 4);
+          float v[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[e] = 0.f + eb[rr][8 * j + e];
+          Wht128x8Signed(v);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[e] *= WhtLaneSign() * (kHadNorm * sv[e]);
+          const int r = rb * 16 + rr;
+          if (r < nrows) StoreF8(pl.y + (size_t)(row0 + r) * pl.ldy + c0, v);
+        }
+        __builtin_amdgcn_wave_barrier();
+      }
+      return;
+    }
+#pragma unroll
+    for (int i = 0; i < NA; ++i) {
+      const int rb = wave + 4 * i;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int col = (2 * (cpg * 4 + c) + ((lane & 15) >> 3)) * 16 + (lane & 7);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = rb * 16 + 4 * (lane >> 4) + e;
+          if (r < nrows) {
+            float* yr = pl.y + (size_t)(row0 + r) * pl.ldy;
+            yr[col] = acc[i][c][0][e];
+            yr[col + 8] = acc[i][c][1][e];
+          }
+        }
+      }
+    }
+  };
+  using std::integral_constant;
+  [&]<int... Is>(std::integer_sequence<int, Is...>) {
+    const int na = (nrb + 3) / 4;
+    (void)((na <= Is + 1 ? (main_loop(integral_constant<int, Is + 1>{}), true) : false) || ...);
+  }(std::make_integer_sequence<int, NRBW>{});
+}
+
+}  // namespace cx
+

@@ -26,6 +26,7 @@ bool CX_CAT(LaunchGemmPrefillRate, CX_RATE)(int cb, int nrbt, int wpg, dim3 grid
     if (nrbt == 4 && wpg == 16) return go(cbc, IC<4>{}, IC<16>{});
     if (nrbt == 8 && wpg == 4) return go(cbc, IC<8>{}, IC<4>{});
     if (nrbt == 8 && wpg == 8) return go(cbc, IC<8>{}, IC<8>{});
+    if (nrbt == 12 && wpg == 4) return go(cbc, IC<12>{}, IC<4>{});
     return false;
   };
   if (cb == kCbMul1) return shape(IC<kCbMul1>{});
@@ -37,3 +38,22 @@ bool CX_CAT(LaunchGemmPrefillRate, CX_RATE)(int cb, int nrbt, int wpg, dim3 grid
 }
 
 }  // namespace cx
+
+namespace cx {
+
+bool CX_CAT(LaunchGemmTallRate, CX_RATE)(int cb, dim3 grid, const GemmArgs& g, hipStream_t s) {
+  constexpr int K2 = CX_RATE;
+  auto go = [&](auto cbc) {
+    hipLaunchKernelGGL((Exl3GemmTallKernel<K2, decltype(cbc)::value, kTallRowBlocksPerWave>), grid, dim3(256), 0, s, g);
+    return true;
+  };
+  if (cb == kCbMul1) return go(IC<kCbMul1>{});
+  if constexpr (K2 % 2 == 0) {
+    if (cb == kCbMcg) return go(IC<kCbMcg>{});
+    if (cb == kCb3Inst) return go(IC<kCb3Inst>{});
+  }
+  return false;
+}
+
+}  // namespace cx
+

@@ -585,7 +585,7 @@ namespace cx {
 
 struct MoeSizes {
   int M, P, n, nsh, chunk, nrb, wpg, max_entries, ntiles;
-  bool small, prefill;
+  bool small, prefill, tall;
   size_t off_sel, off_wts, off_counts, off_offsets, off_pairs, off_rows, off_inv, off_rexp, off_ent, off_nent, off_tiles;
   size_t off_xg, off_xu, off_yg, off_yu, off_xd, off_yd, total;
 };
@@ -596,6 +596,7 @@ struct MoeSizes {
 // (4 | 8 | 16).
 struct PrefillShape {
   int nrb, wpg;
+  int kernel;  // prefill GEMM: 0 register-blocked, 1 tall, -1 by the rows per expert
 };
 PrefillShape PrefillConfig() {
   static const PrefillShape ps = [] {
@@ -603,9 +604,10 @@ PrefillShape PrefillConfig() {
       const char* e = std::getenv(k);
       return e ? std::atoi(e) : d;
     };
-    const int nrb = env("CX_PREFILL_NRB", 4) == 8 ? 8 : 4;
+    const int nv = env("CX_PREFILL_NRB", 4);
+    const int nrb = nv == 8 || nv == 12 ? nv : 4;
     const int w = env("CX_PREFILL_WPG", 4);
-    return PrefillShape{nrb, w == 16 && nrb == 4 ? 16 : w == 4 ? 4 : 8};
+    return PrefillShape{nrb, w == 16 && nrb == 4 ? 16 : w == 4 || nrb == 12 ? 4 : 8, env("CX_PREFILL_GEMM", -1)};
   }();
   return ps;
 }
@@ -620,6 +622,11 @@ MoeSizes PlanMoe(const cx_moe_plan* pl, int M, int mode) {
   const PrefillShape ps = PrefillConfig();
   s.nrb = decode ? 1 : ps.nrb;
   s.wpg = decode ? 4 : ps.wpg;
+  // The tall GEMM when experts average at least 96 rows (one decode then serves up to 192
+  // rows); below that most entries fit the register-blocked GEMM's 64 rows.
+  const int kern = ps.kernel >= 0 ? ps.kernel : (long)M * pl->topk >= 96L * pl->E ? 1 : 0;
+  s.tall = !decode && kern == 1;
+  if (s.tall) s.nrb = 4 * kTallRowBlocksPerWave;
   // Decode: one 16-row block per entry; prefill: every row of an entry shares each decoded tile.
   s.chunk = 16 * s.nrb;
   s.nsh = (M + s.chunk - 1) / s.chunk;
@@ -733,8 +740,9 @@ bool LaunchExpertGemm(const cx_moe_plan* pl, const MoeSizes& sz, bool gate_up, c
   const int k2r = gate_up ? pl->k2_gu : pl->k2_d, cbr = gate_up ? pl->cb_gu : pl->cb_d;
   const int k2s = gate_up ? pl->k2_sgu : pl->k2_sd, cbs = gate_up ? pl->cb_sgu : pl->cb_sd;
   const int wpg = g.ncp % sz.wpg == 0 ? sz.wpg : 4;
-  const int cpg = sz.prefill ? g.ncp / wpg : g.ncp / (4 / ksw);
+  const int cpg = sz.tall ? g.ncp / 4 : sz.prefill ? g.ncp / wpg : g.ncp / (4 / ksw);
   auto launch = [&](int k2, int cb, int ny) {
+    if (sz.tall) return LaunchGemmTall(k2, cb, dim3(cpg, (ny + 7) / 8 * 8, planes), g, s);
     if (sz.prefill)  // entry-major XCD placement needs the entry count padded to 8
       return LaunchGemmPrefill(k2, cb, sz.nrb, wpg, dim3(cpg, (ny + 7) / 8 * 8, planes), g, s);
     return LaunchGemm(k2, cb, sz.nrb, ksw, 4, dim3(cpg, ny, planes), g, s);
