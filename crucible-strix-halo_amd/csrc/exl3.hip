@@ -256,7 +256,7 @@ int RunGroup(const cx_exl3_job* jobs, int n, int M, char* ws, hipStream_t s) {
     out_items += M * (O / 128);
     GemmArgs& g = gs[j];
     g = GemmArgs{};
-    g.plane[0] = GemmPlane{nullptr, xp, part, I, O, (long long)M * O, 0};
+    g.plane[0] = GemmPlane{nullptr, xp, part, I, O, (long long)M * O, 0, nullptr};
     g.plane[1] = g.plane[0];
     g.entries = nullptr;
     g.n_entries = nullptr;

@@ -60,8 +60,40 @@ struct GemmPlane {
   float* y;            // fp32 outputs; row r at y + r * ldy (+ K segment * seg_stride)
   int ldx, ldy;
   long long seg_stride;
-  int epi;  // 0: raw sums y_h; 1: output transform WHT128(y_h) * norm * svh (needs KSW = 1, S = 1)
+  // 0: raw sums y_h; 1: output transform WHT128(y_h) * norm * svh, fp32 (needs KSW = 1,
+  // S = 1); 2: the same transform stored as fp16 with a power-of-two scale per (row,
+  // 128-column block): y as __half rows of ldy halves, the scales in ysc [row][O / 128].
+  int epi;
+  float* ysc;
 };
+
+// Stores one row's 8 output values of a 128-column block after the output transform; the
+// 16 lanes of a DPP row hold the block (epi 1 or 2 of GemmPlane).  fp16 form: the block is
+// divided by 2^sh, sh = floor(log2 max|v|) - 14 (exact: a power of two), so its largest
+// magnitude lies in [2^14, 2^15) and every value is rounded to fp16 once, with the full
+// fp16 precision and no overflow; a block holding inf or NaN is stored unscaled.
+__device__ __forceinline__ void StoreBlockRow(const GemmPlane& pl, size_t row, int c0, int O, const float v[8]) {
+  if (pl.epi == 1) {
+    StoreF8(pl.y + row * pl.ldy + c0, v);
+    return;
+  }
+  float m = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[i]));
+  m = fmaxf(m, Dpp<kDppQuadSwap1>(m));
+  m = fmaxf(m, Dpp<kDppQuadSwap2>(m));
+  m = fmaxf(m, Dpp<kDppRowHalfMirror>(m));
+  m = fmaxf(m, Dpp<kDppRowMirror>(m));
+  int sh = 0;
+  if (m > 0.f && m <= 3.4e38f) sh = min(max((int)((__float_as_uint(m) >> 23) & 0xff) - 127 - 14, -100), 100);
+  const float inv = ldexpf(1.f, -sh);
+  uint32_t h[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) h[k] = __builtin_bit_cast(uint32_t, __floats2half2_rn(v[2 * k] * inv, v[2 * k + 1] * inv));
+  __half* d = reinterpret_cast<__half*>(pl.y) + row * pl.ldy + c0;
+  *reinterpret_cast<uint4*>(d) = make_uint4(h[0], h[1], h[2], h[3]);
+  if ((threadIdx.x & 15) == 0) pl.ysc[row * (O / 128) + c0 / 128] = ldexpf(1.f, sh);
+}
 
 struct GemmArgs {
   GemmPlane plane[2];
@@ -524,7 +556,7 @@ __global__ void __launch_bounds__(64 * WPG) Exl3GemmPrefillKernel(GemmArgs g) {
     (void)((na == Is + 1 ? (main_loop(integral_constant<int, Is + 1>{}), true) : false) || ...);
   }(std::make_integer_sequence<int, NRBT>{});
 
-  if (pl.epi == 1) {
+  if (pl.epi >= 1) {
     // Output transform per 128-column block: stage y_h rows in LDS, ER rows at a time
     // (reusing the activation tile area), WHT128 * norm * svh per row.
     float(*eb)[132] = reinterpret_cast<float(*)[132]>(smem);
@@ -563,7 +595,7 @@ __global__ void __launch_bounds__(64 * WPG) Exl3GemmPrefillKernel(GemmArgs g) {
           Wht128x8Signed(v);
 #pragma unroll
           for (int e = 0; e < 8; ++e) v[e] *= WhtLaneSign() * (kHadNorm * sv[e]);
-          StoreF8(pl.y + (size_t)(row0 + r0 + rr) * pl.ldy + c0, v);
+          StoreBlockRow(pl, (size_t)(row0 + r0 + rr), c0, g.ncp * 32, v);
         }
         __syncthreads();
       }
@@ -748,7 +780,7 @@ Exl3GemmTallKernel(GemmArgs g) {
     }
     __syncthreads();  // every wave is done with the B buffers: the epilogue reuses them
 
-    if (pl.epi == 1) {
+    if (pl.epi >= 1) {
       // Output transform per row: the wave holds all 128 columns of its row blocks.
       // Stage one row block (16 x 128 fp32) in the wave's slab, then WHT128 * norm * svh.
       float(*eb)[132] = reinterpret_cast<float(*)[132]>(smem + wave * ER * 132 * 4);
@@ -779,7 +811,7 @@ Exl3GemmTallKernel(GemmArgs g) {
 #pragma unroll
           for (int e = 0; e < 8; ++e) v[e] *= WhtLaneSign() * (kHadNorm * sv[e]);
           const int r = rb * 16 + rr;
-          if (r < nrows) StoreF8(pl.y + (size_t)(row0 + r) * pl.ldy + c0, v);
+          if (r < nrows) StoreBlockRow(pl, (size_t)(row0 + r), c0, g.ncp * 32, v);
         }
         __builtin_amdgcn_wave_barrier();
       }

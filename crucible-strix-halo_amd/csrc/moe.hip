@@ -528,12 +528,14 @@ struct HcArgs {
 
 // Combine: per row, slots 0..topk-1 in selection order then the shared expert:
 // y += w_k * d_k, fp32, where d_k = WHT(y_h) * (norm * svh) came out of the down GEMM's
-// epilogue.  engine/layers/moe_rows.h:634-682.  HC: accumulate into the residual streams
-// instead of storing y (engine/layers/moe_rows.h:672-681).
-template <bool HC>
-__global__ void __launch_bounds__(256) MoeCombineKernel(const float* __restrict__ pd, const float* __restrict__ wts,
-                                                        const int* __restrict__ inv, int M, int topk, int H,
-                                                        float* __restrict__ y, HcArgs hc) {
+// epilogue: fp32 rows (decode), or fp16 rows with a power-of-two scale per 128-column
+// block (F16, prefill: the reference's prefill keeps d_k in fp16 too,
+// engine/layers/prefill_moe.h:648).  engine/layers/moe_rows.h:634-682.  HC: accumulate
+// into the residual streams instead of storing y (engine/layers/moe_rows.h:672-681).
+template <bool HC, bool F16>
+__global__ void __launch_bounds__(256) MoeCombineKernel(const void* __restrict__ pd, const float* __restrict__ psc,
+                                                        const float* __restrict__ wts, const int* __restrict__ inv,
+                                                        int M, int topk, int H, float* __restrict__ y, HcArgs hc) {
   const int nq = H / 4;
   const int item = blockIdx.x * blockDim.x + threadIdx.x;
   if (item >= M * nq) return;
@@ -542,7 +544,15 @@ __global__ void __launch_bounds__(256) MoeCombineKernel(const float* __restrict_
 #pragma unroll 4
   for (int k = 0; k <= topk; ++k) {
     const int p = k < topk ? inv[r * topk + k] : M * topk + r;
-    const float4 d = *reinterpret_cast<const float4*>(pd + (size_t)p * H + c0);
+    float4 d;
+    if constexpr (F16) {
+      const uint2 u = *reinterpret_cast<const uint2*>(static_cast<const __half*>(pd) + (size_t)p * H + c0);
+      const float sc = psc[(size_t)p * (H / 128) + c0 / 128];
+      const float2 a = __half22float2(__builtin_bit_cast(__half2, u.x)), b = __half22float2(__builtin_bit_cast(__half2, u.y));
+      d = make_float4(a.x * sc, a.y * sc, b.x * sc, b.y * sc);
+    } else {
+      d = *reinterpret_cast<const float4*>(static_cast<const float*>(pd) + (size_t)p * H + c0);
+    }
     const float w = wts[(size_t)r * (topk + 1) + k];
     acc.x += w * d.x;
     acc.y += w * d.y;
@@ -587,7 +597,7 @@ struct MoeSizes {
   int M, P, n, nsh, chunk, nrb, wpg, max_entries, ntiles;
   bool small, prefill, tall;
   size_t off_sel, off_wts, off_counts, off_offsets, off_pairs, off_rows, off_inv, off_rexp, off_ent, off_nent, off_tiles;
-  size_t off_xg, off_xu, off_yg, off_yu, off_xd, off_yd, total;
+  size_t off_xg, off_xu, off_yg, off_yu, off_xd, off_yd, off_ysc, total;
 };
 
 // Prefill GEMM shape: a workgroup of wpg waves covers 16 nrb rows x 32 wpg columns (every
@@ -655,7 +665,8 @@ MoeSizes PlanMoe(const cx_moe_plan* pl, int M, int mode) {
   s.off_yg = take((size_t)s.P * pl->I * 4);
   s.off_yu = take((size_t)s.P * pl->I * 4);
   s.off_xd = take((size_t)s.P * pl->I * 2);
-  s.off_yd = take((size_t)s.P * pl->H * 4);
+  s.off_yd = take((size_t)s.P * pl->H * (s.prefill ? 2 : 4));
+  s.off_ysc = take(s.prefill ? (size_t)s.P * (pl->H / 128) * 4 : 0);
   s.total = o;
   return s;
 }
@@ -717,7 +728,8 @@ int LaunchGroup(const int* sel, GroupOut& o, int* tile_counts, int ntiles, hipSt
 // entries [nsh, n_entries).  Routed and shared matrices with different rates go in
 // separate launches.
 bool LaunchExpertGemm(const cx_moe_plan* pl, const MoeSizes& sz, bool gate_up, const __half* xa, const __half* xb,
-                      float* ya, float* yb, const int4* ent, const int* nent, const int* xmap, hipStream_t s) {
+                      float* ya, float* yb, float* ysc, const int4* ent, const int* nent, const int* xmap,
+                      hipStream_t s) {
   GemmArgs g{};
   g.xmap = xmap;
   g.xmap_n = sz.n;
@@ -727,12 +739,14 @@ bool LaunchExpertGemm(const cx_moe_plan* pl, const MoeSizes& sz, bool gate_up, c
   g.S = 1;
   g.entries = ent;
   if (gate_up) {
-    g.plane[0] = GemmPlane{pl->tb.gate, xa, ya, in, out, 0, 0};
-    g.plane[1] = GemmPlane{pl->tb.up, xb, yb, in, out, 0, 0};
+    g.plane[0] = GemmPlane{pl->tb.gate, xa, ya, in, out, 0, 0, nullptr};
+    g.plane[1] = GemmPlane{pl->tb.up, xb, yb, in, out, 0, 0, nullptr};
   } else {
     // The down projection's output transform runs in the GEMM epilogue (a workgroup
     // holds one whole 128-column block), so the combine is a plain weighted sum.
-    g.plane[0] = GemmPlane{pl->tb.down, xa, ya, in, out, 0, 1};
+    // Prefill stores it as fp16 rows with a scale per 128-column block (half the bytes).
+    g.plane[0] = sz.prefill ? GemmPlane{pl->tb.down, xa, ya, in, out, 0, 2, ysc}
+                            : GemmPlane{pl->tb.down, xa, ya, in, out, 0, 1, nullptr};
     g.plane[1] = g.plane[0];
   }
   const int ksw = gate_up ? 4 : 1;
@@ -949,6 +963,7 @@ int MoeForward(const cx_moe_plan* pl, const void* x, int32_t x_dtype, int32_t ld
   float* yu = reinterpret_cast<float*>(ws + sz.off_yu);
   __half* xd = reinterpret_cast<__half*>(ws + sz.off_xd);
   float* yd = reinterpret_cast<float*>(ws + sz.off_yd);
+  float* ysc = reinterpret_cast<float*>(ws + sz.off_ysc);
 
   cx_moe_plan* mp = const_cast<cx_moe_plan*>(pl);
   auto mark = [&]() {
@@ -979,23 +994,32 @@ int MoeForward(const cx_moe_plan* pl, const void* x, int32_t x_dtype, int32_t ld
                        xg, xu);
   }
   mark();
-  if (!LaunchExpertGemm(pl, sz, true, xg, xu, yg, yu, ent, nent, front ? pairs : nullptr, s)) return CX_E_UNSUPPORTED;
+  if (!LaunchExpertGemm(pl, sz, true, xg, xu, yg, yu, nullptr, ent, nent, front ? pairs : nullptr, s))
+    return CX_E_UNSUPPORTED;
   mark();
   {
     hipLaunchKernelGGL(MoeMidKernel, dim3((unsigned)((sz.P + 3) / 4)), dim3(256), 0, s, yg, yu, rexp,
                        pl->tb, M, pl->topk, pl->E, pl->I, xd);
   }
   mark();
-  if (!LaunchExpertGemm(pl, sz, false, xd, nullptr, yd, nullptr, ent, nent, nullptr, s)) return CX_E_UNSUPPORTED;
+  if (!LaunchExpertGemm(pl, sz, false, xd, nullptr, yd, nullptr, ysc, ent, nent, nullptr, s)) return CX_E_UNSUPPORTED;
   mark();
   {
     const long items = (long)M * (pl->H / 4);
-    if (hc)
-      hipLaunchKernelGGL(MoeCombineKernel<true>, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, s, yd, wts, inv,
-                         M, pl->topk, pl->H, nullptr, *hc);
+    const dim3 grid((unsigned)((items + 255) / 256));
+    const HcArgs h = hc ? *hc : HcArgs{};
+    if (hc && sz.prefill)
+      hipLaunchKernelGGL((MoeCombineKernel<true, true>), grid, dim3(256), 0, s, yd, ysc, wts, inv, M, pl->topk, pl->H,
+                         nullptr, h);
+    else if (hc)
+      hipLaunchKernelGGL((MoeCombineKernel<true, false>), grid, dim3(256), 0, s, yd, ysc, wts, inv, M, pl->topk, pl->H,
+                         nullptr, h);
+    else if (sz.prefill)
+      hipLaunchKernelGGL((MoeCombineKernel<false, true>), grid, dim3(256), 0, s, yd, ysc, wts, inv, M, pl->topk, pl->H,
+                         y, h);
     else
-      hipLaunchKernelGGL(MoeCombineKernel<false>, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, s, yd, wts, inv,
-                         M, pl->topk, pl->H, y, HcArgs{});
+      hipLaunchKernelGGL((MoeCombineKernel<false, false>), grid, dim3(256), 0, s, yd, ysc, wts, inv, M, pl->topk, pl->H,
+                         y, h);
   }
   mark();
   return LaunchStatus();

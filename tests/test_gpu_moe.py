@@ -213,9 +213,11 @@ def test_config4_prefill_subset(ops, layer512):
     print(f"config4 rel_l2={e:.3e} max_abs={np.abs(y[rows] - ref).max():.3e}")
     assert e <= 1e-3
     # Decode and prefill plans agree on the same rows: they sum K in different fp32 orders,
-    # which the fp16 rounding points of the mid step can amplify to ~1e-4 at most.
+    # which the fp16 rounding points of the mid step can amplify to ~1e-4, and the prefill
+    # keeps the down outputs in fp16 (one rounding, 2^-12 relative rms) as the reference's
+    # prefill does (engine/layers/prefill_moe.h:648).
     y2, _, _ = run_layer(layer512, x[:40], lg[:40], 1)
-    assert rel_l2(y2, y[:40]) <= 2e-4
+    assert rel_l2(y2, y[:40]) <= 5e-4
 
 
 @pytest.mark.parametrize("mode", [1, 2])
