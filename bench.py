@@ -33,6 +33,9 @@ MFMA_F16_PEAK_TFS = 2500.0  # MI355X dense fp16 MFMA, published (no sparsity)
 E, H, IE, TOPK = 512, 2048, 512, 10
 
 
+GATE_UP_KERNEL = "Exl3GemmKernel<8, 2, 1, 4, 2>"  # the decode gate/up instantiation at 4.0 bpw (mul1)
+
+
 def matrix_bytes(i, o, k2):
     return i * o * k2 // 16 + 2 * i + 2 * o
 
@@ -348,53 +351,147 @@ def bench_long(seed, steps=3, head_copies=5, head_calls=20):
     return out
 
 
+def bench_r1(plans, seed, calls=200, warmup=50):
+    """R = 1 decode (one row, the serial-decode case): per-layer latency, eager (events
+    around each call) and replayed from one HIP graph, beside the launch-bound floor: the
+    same number of dependent minimal kernels (torch's one-wave spin kernel, 0 cycles)
+    timed the same two ways."""
+    import numpy as np
+    import torch
+    from exl3moe import CX_MOE_DECODE
+    from exl3moe.trace import EventTimer
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    xs = [torch.randn(1, H, generator=g, device="cuda").half() for _ in range(8)]
+    lgs = [torch.randn(1, E + 1, generator=g, device="cuda") for _ in range(8)]
+    ws = torch.empty(max(p.workspace_size(1, CX_MOE_DECODE) for p in plans), dtype=torch.uint8, device="cuda")
+    y = torch.empty(1, H, dtype=torch.float32, device="cuda")
+    n_launch = 6  # route, grouping + input transforms, gate/up, mid, down, combine
+
+    def call(i):
+        plans[i % len(plans)](xs[i % 8], lgs[i % 8], mode=CX_MOE_DECODE, workspace=ws, y=y)
+
+    def floor_call(i):
+        for _ in range(n_launch):
+            torch.cuda._sleep(0)
+
+    def eager(fn):
+        for i in range(warmup):
+            fn(i)
+        torch.cuda.synchronize()
+        t = EventTimer(calls, torch.cuda.current_stream().cuda_stream)
+        for i in range(calls):
+            t.mark()
+            fn(i)
+        t.mark()
+        v = np.array(t.ms()) * 1000
+        t.close()
+        return v
+
+    def graphed(fn, n=50):
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            for i in range(n):
+                fn(i)
+        gr.replay()
+        torch.cuda.synchronize()
+        tg = EventTimer(5, torch.cuda.current_stream().cuda_stream)
+        for _ in range(5):
+            tg.mark()
+            gr.replay()
+        tg.mark()
+        us = float(np.min(tg.ms())) * 1000 / n
+        tg.close()
+        del gr
+        return us
+
+    out = {"workload": "config-3 layer at R = 1 (one row, E=512 top-10 + shared, 4.0 bpw), rotating over the "
+                       "seeded layers", "launches": n_launch}
+    out["eager_us"] = pct(eager(call))
+    out["floor_eager_us"] = pct(eager(floor_call))
+    try:
+        out["graph_us"] = round(graphed(call), 2)
+        out["floor_graph_us"] = round(graphed(floor_call), 2)
+    except RuntimeError as e:
+        print(f"bench.py: graph capture at R = 1 failed: {e}", file=sys.stderr)
+    return out
+
+
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(plan, batch, seconds):
-    """The oracle (C restatement, OpenMP) on the host cores over whole steps of the same
-    workload: decode of the routed experts' weights + the layer math, until `seconds`."""
+    """The oracle (C restatement, OpenMP) on the host cores over whole decode steps of the
+    same workload: decode of the routed experts' weights + the layer math.  One untimed
+    warm-up step, then >= 5 timed steps at the process's OpenMP thread count (median
+    reported), then one step on a single thread; the sample is bounded by `seconds`."""
     import numpy as np
     sys.path.insert(0, str(ROOT / "oracle"))
     import oracle as O
     offs, x, lg = batch
     xh = x.cpu().numpy()
     lgh = lg.cpu().numpy()
+    sel, wts = O.route(lgh, E, TOPK)
+    used = sorted(set(sel.ravel().tolist()))
 
-    # Weights leave the GPU before the clock starts; decode + math is timed.
-    rows = 0
-    steps = 0
-    elapsed = 0.0
-    while steps == 0 or elapsed < seconds:
-        sel, wts = O.route(lgh, E, TOPK)
-        used = sorted(set(sel.ravel().tolist()))
-        def host(t):
-            return (t.cpu().numpy() if hasattr(t, "cpu") else t).view(np.uint16)
-        raw = {e: {k: (host(plan._experts[e][k].trellis), plan._experts[e][k]) for k in ("gate", "up", "down")}
-               for e in used}
-        sh_raw = {k: (host(plan._shared[k].trellis), plan._shared[k]) for k in ("gate", "up", "down")}
+    def host(t):
+        return (t.cpu().numpy() if hasattr(t, "cpu") else t).view(np.uint16)
+
+    # Weights leave the GPU before any clock starts; decode + math is timed.
+    raw = {e: {k: (host(plan._experts[e][k].trellis), plan._experts[e][k]) for k in ("gate", "up", "down")}
+           for e in used}
+    sh_raw = {k: (host(plan._shared[k].trellis), plan._shared[k]) for k in ("gate", "up", "down")}
+
+    def one_step():
         t1 = time.perf_counter()
+
+        def dec(tr, lin):
+            return {"w": O.reconstruct_inner(tr, lin.k2 / 2, lin.codebook), "s": lin.suh.cpu().numpy(),
+                    "v": lin.svh.cpu().numpy()}
         experts = {}
         for e in used:
             d = {}
             for n, key in (("g", "gate"), ("u", "up"), ("d", "down")):
-                tr, lin = raw[e][key]
-                d["w" + n] = O.reconstruct_inner(tr, lin.k2 / 2, lin.codebook)
-                d["s" + n] = lin.suh.cpu().numpy()
-                d["v" + n] = lin.svh.cpu().numpy()
+                p = dec(*raw[e][key])
+                d["w" + n], d["s" + n], d["v" + n] = p["w"], p["s"], p["v"]
             experts[e] = d
         shd = {}
         for n, key in (("g", "gate"), ("u", "up"), ("d", "down")):
-            tr, lin = sh_raw[key]
-            shd["w" + n] = O.reconstruct_inner(tr, lin.k2 / 2, lin.codebook)
-            shd["s" + n] = lin.suh.cpu().numpy()
-            shd["v" + n] = lin.svh.cpu().numpy()
+            p = dec(*sh_raw[key])
+            shd["w" + n], shd["s" + n], shd["v" + n] = p["w"], p["s"], p["v"]
         dummy = experts[used[0]]
         O.moe_layer([experts.get(e, dummy) for e in range(E)], shd, xh, sel, wts)
-        elapsed += time.perf_counter() - t1
-        rows += xh.shape[0]
-        steps += 1
-    return {"value": rows / elapsed, "unit": "tokens/s", "cores": O.num_threads(), "kind": "port",
-            "sample": f"{steps} decode step(s) of config 3 ({xh.shape[0]} rows each, {len(used)} distinct experts "
-                      f"in the last): host decode of the routed experts' weights + the layer math, oracle/exl3_oracle.c "
-                      f"with OpenMP; {elapsed:.1f} s"}
+        return time.perf_counter() - t1
+
+    threads = O.num_threads()
+    t_start = time.perf_counter()
+    one_step()  # warm-up (page faults, OpenMP pool)
+    runs = []
+    while len(runs) < 5 or (time.perf_counter() - t_start < seconds / 2 and len(runs) < 50):
+        runs.append(one_step())
+    O.set_num_threads(1)
+    try:
+        single = one_step()
+    finally:
+        O.set_num_threads(threads)
+    med = float(np.median(runs))
+    rows = xh.shape[0]
+    return {"value": round(rows / med, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "cpu_model": _cpu_model(), "nproc": os.cpu_count(),
+            "affinity_cpus": len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else None,
+            "omp_threads": threads, "runs": len(runs),
+            "step_s": {"median": round(med, 4), "min": round(min(runs), 4), "max": round(max(runs), 4)},
+            "single_thread": {"value": round(rows / single, 3), "unit": "tokens/s", "step_s": round(single, 3)},
+            "sample": f"config-3 decode step of {rows} rows ({len(used)} distinct routed experts + the shared one): "
+                      f"host decode of their weights + the layer math (oracle/exl3_oracle.c, OpenMP); median of "
+                      f"{len(runs)} timed steps after one warm-up step, then one step on 1 thread"}
 
 
 def main():
@@ -434,11 +531,20 @@ def main():
     gu_achieved = float(gu_bytes.sum() / (gu.sum() / 1000)) / 1e9
     layer_bytes = np.array([(u + 1) * eb + m * H * 2 + m * H * 4 + m * (E + 1) * 4 for u, m in zip(r["distinct"], r["M"])])
     layer_gbs = float(layer_bytes.sum() / r["wall_s"]) / 1e9
-    traffic = None
+    # HBM bytes per gate/up launch: not measurable inside this run (counter collection needs
+    # rocprofv3); taken from the committed counter profile of the same kernel and workload,
+    # with its provenance beside it (traffic_source), and dropped when the profile names
+    # another kernel instantiation than the one this build launches.
+    traffic, traffic_src = None, None
     tf = ROOT / "profiles" / "traffic_decode_gate_up.json"
     if tf.exists():
         try:
-            traffic = json.loads(tf.read_text()).get("hbm_bytes_per_launch")
+            tj = json.loads(tf.read_text())
+            if tj.get("kernel") == GATE_UP_KERNEL:
+                traffic = tj.get("hbm_bytes_per_launch")
+                traffic_src = {"file": "profiles/traffic_decode_gate_up.json", "kernel": tj.get("kernel"),
+                               "command": tj.get("command"), "note": "measured by rocprofv3 --pmc in a separate "
+                               "run of this bench workload, FETCH_SIZE scaled by a device-copy calibration"}
         except Exception:
             traffic = None
     out = {
@@ -461,7 +567,7 @@ def main():
                    "distinct_experts_mean": round(float(np.mean(r["distinct"])), 1)},
         "roofline": {"bound": "hbm", "kernel": "Exl3GemmKernel (gate/up)", "achieved": round(gu_achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gu_achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic, "avg_us": round(float(gu.mean() * 1000), 2),
+                     "traffic": traffic, "traffic_source": traffic_src, "avg_us": round(float(gu.mean() * 1000), 2),
                      "algorithmic_bytes_per_launch": int(gu_bytes.mean())},
         "layer": {"algorithmic_GBps": round(layer_gbs, 1), "frac_hbm": round(layer_gbs / HBM_PEAK_GBS, 4),
                   "traced_step_us": pct(st.sum(1) * 1000),
@@ -490,6 +596,7 @@ def main():
             "stage_us_mean": {n: round(float(stp[:, i].mean() * 1000), 2) for i, n in enumerate(
                 ["route", "group", "input", "gate_up", "mid", "down", "combine"])},
         }
+    out["decode_r1"] = bench_r1(plans, args.seed + 500)
     if not args.no_linear:
         out["linear"] = bench_linear(args.seed + 300)
     if not args.no_long:

@@ -442,3 +442,13 @@ int or_num_threads(void) {
   return 1;
 #endif
 }
+
+/* Sets the OpenMP thread count of later calls (timing runs at 1 thread and at all). */
+void or_set_num_threads(int n) {
+#ifdef _OPENMP
+  extern void omp_set_num_threads(int);
+  omp_set_num_threads(n > 0 ? n : 1);
+#else
+  (void)n;
+#endif
+}

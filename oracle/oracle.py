@@ -60,6 +60,8 @@ def lib() -> ctypes.CDLL:
         L.or_moe_layer.argtypes = [P, P, P, ctypes.c_long, ctypes.c_int, ctypes.c_int, ctypes.c_int, P, P, P]
         L.or_expert_rows.argtypes = [P, P, ctypes.c_long, ctypes.c_int, ctypes.c_int, P]
         L.or_num_threads.restype = ctypes.c_int
+        L.or_set_num_threads.argtypes = [ctypes.c_int]
+        L.or_set_num_threads.restype = None
         L.or_valid_k2.argtypes = [ctypes.c_int]
         L.or_valid_k2.restype = ctypes.c_int
         _lib = L
@@ -228,6 +230,10 @@ def expert_rows(ex: dict, x: np.ndarray) -> np.ndarray:
 
 def num_threads() -> int:
     return int(lib().or_num_threads())
+
+
+def set_num_threads(n: int) -> None:
+    lib().or_set_num_threads(int(n))
 
 
 # ---- the reference's own lane-window code (oracle/_ref), when it was built ----
