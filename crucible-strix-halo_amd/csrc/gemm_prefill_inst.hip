@@ -26,7 +26,6 @@ bool CX_CAT(LaunchGemmPrefillRate, CX_RATE)(int cb, int nrbt, int wpg, dim3 grid
     if (nrbt == 4 && wpg == 16) return go(cbc, IC<4>{}, IC<16>{});
     if (nrbt == 8 && wpg == 4) return go(cbc, IC<8>{}, IC<4>{});
     if (nrbt == 8 && wpg == 8) return go(cbc, IC<8>{}, IC<8>{});
-    if (nrbt == 12 && wpg == 4) return go(cbc, IC<12>{}, IC<4>{});
     return false;
   };
   if (cb == kCbMul1) return shape(IC<kCbMul1>{});

@@ -614,10 +614,9 @@ PrefillShape PrefillConfig() {
       const char* e = std::getenv(k);
       return e ? std::atoi(e) : d;
     };
-    const int nv = env("CX_PREFILL_NRB", 4);
-    const int nrb = nv == 8 || nv == 12 ? nv : 4;
+    const int nrb = env("CX_PREFILL_NRB", 4) == 8 ? 8 : 4;
     const int w = env("CX_PREFILL_WPG", 4);
-    return PrefillShape{nrb, w == 16 && nrb == 4 ? 16 : w == 4 || nrb == 12 ? 4 : 8, env("CX_PREFILL_GEMM", -1)};
+    return PrefillShape{nrb, w == 16 && nrb == 4 ? 16 : w == 4 ? 4 : 8, env("CX_PREFILL_GEMM", -1)};
   }();
   return ps;
 }
