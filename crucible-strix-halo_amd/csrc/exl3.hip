@@ -191,19 +191,19 @@ bool LaunchGemm(int k2, int cb, int nrb, int ksw, int u, dim3 grid, const GemmAr
   }
 }
 
-bool LaunchGemmPrefill(int k2, int cb, int nrbt, int wpg, dim3 grid, const GemmArgs& g, hipStream_t s) {
+bool LaunchGemmPrefill(int k2, int cb, int nrbt, int wpg, bool mid, dim3 grid, const GemmArgs& g, hipStream_t s) {
   switch (k2) {
-    case 2: return LaunchGemmPrefillRate2(cb, nrbt, wpg, grid, g, s);
-    case 3: return LaunchGemmPrefillRate3(cb, nrbt, wpg, grid, g, s);
-    case 4: return LaunchGemmPrefillRate4(cb, nrbt, wpg, grid, g, s);
-    case 5: return LaunchGemmPrefillRate5(cb, nrbt, wpg, grid, g, s);
-    case 6: return LaunchGemmPrefillRate6(cb, nrbt, wpg, grid, g, s);
-    case 7: return LaunchGemmPrefillRate7(cb, nrbt, wpg, grid, g, s);
-    case 8: return LaunchGemmPrefillRate8(cb, nrbt, wpg, grid, g, s);
-    case 10: return LaunchGemmPrefillRate10(cb, nrbt, wpg, grid, g, s);
-    case 12: return LaunchGemmPrefillRate12(cb, nrbt, wpg, grid, g, s);
-    case 14: return LaunchGemmPrefillRate14(cb, nrbt, wpg, grid, g, s);
-    case 16: return LaunchGemmPrefillRate16(cb, nrbt, wpg, grid, g, s);
+    case 2: return LaunchGemmPrefillRate2(cb, nrbt, wpg, mid, grid, g, s);
+    case 3: return LaunchGemmPrefillRate3(cb, nrbt, wpg, mid, grid, g, s);
+    case 4: return LaunchGemmPrefillRate4(cb, nrbt, wpg, mid, grid, g, s);
+    case 5: return LaunchGemmPrefillRate5(cb, nrbt, wpg, mid, grid, g, s);
+    case 6: return LaunchGemmPrefillRate6(cb, nrbt, wpg, mid, grid, g, s);
+    case 7: return LaunchGemmPrefillRate7(cb, nrbt, wpg, mid, grid, g, s);
+    case 8: return LaunchGemmPrefillRate8(cb, nrbt, wpg, mid, grid, g, s);
+    case 10: return LaunchGemmPrefillRate10(cb, nrbt, wpg, mid, grid, g, s);
+    case 12: return LaunchGemmPrefillRate12(cb, nrbt, wpg, mid, grid, g, s);
+    case 14: return LaunchGemmPrefillRate14(cb, nrbt, wpg, mid, grid, g, s);
+    case 16: return LaunchGemmPrefillRate16(cb, nrbt, wpg, mid, grid, g, s);
     default: return false;
   }
 }

@@ -112,7 +112,41 @@ struct GemmArgs {
   // (rows at or above xmap_n read row p).  Decode GEMM only.
   const int* xmap;
   int xmap_n;
+  // Prefill gate/up with the mid fused in (Exl3GemmPrefillKernel<..., MID = true>): the
+  // down projection's packed input scales [E + 1][O] and its input rows xd [rows][O] fp16
+  // (MFMA row order), row p at xd + p * O.
+  const __half* mid_suh;
+  __half* mid_xd;
 };
+
+// The mid of one row's 128-column block on 16 lanes (lane j: columns c0 + 8j..8j+7): the
+// gate and up output transforms of the raw sums gv, uv (fp32: WHT128 * norm * svh), then
+// RoundH(RoundH(SiLU(g) * u) * suh_down), WHT128, * norm -> fp16 in MFMA row order at dst
+// (the block's first half).  engine/layers/moe_rows.h:543-566.
+__device__ __forceinline__ void MidBlock(float gv[8], float uv[8], const __half* svg_p, const __half* svu_p,
+                                         const __half* sud_p, __half* dst) {
+  float svg[8], svu[8], sud[8];
+  LoadH8(svg_p, svg);
+  LoadH8(svu_p, svu);
+  LoadH8(sud_p, sud);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    gv[i] = 0.f + gv[i];
+    uv[i] = 0.f + uv[i];
+  }
+  Wht128x8Signed(gv);
+  Wht128x8Signed(uv);
+  const float sg = WhtLaneSign();
+  float v[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float a = gv[i] * (sg * (kHadNorm * svg[i]));
+    const float b = uv[i] * (sg * (kHadNorm * svu[i]));
+    v[i] = RoundH(RoundH(SiLU(a) * b) * sud[i]);
+  }
+  Wht128x8Signed(v);
+  StorePerm32x8(dst, v, kHadNorm * sg);
+}
 
 // Wave-uniform load through the scalar cache (device tables written by earlier launches).
 template <typename T>
@@ -366,8 +400,15 @@ __device__ __forceinline__ GridPos XcdEntryMajor() {
 // tile of a step (16 NRBT rows x 32 inputs) is loaded once into LDS and shared by the
 // waves, so more waves per workgroup read the activations fewer times.  One barrier per
 // step double-buffers the activation tile.
-template <int K2, int CB, int NRBT, int CPWV, int WPG>
-__global__ void __launch_bounds__(64 * WPG) Exl3GemmPrefillKernel(GemmArgs g) {
+//
+// MID: gate and up in one workgroup (2 WPG waves: the first WPG on gate, the others on up,
+// each plane with its own activation tiles), and the mid computed in the epilogue from
+// both planes' sums (MidBlock), written as the down projection's input rows; the raw
+// gate / up sums never leave the workgroup.  Needs 32 WPG CPWV = 128 (one block).
+template <int K2, int CB, int NRBT, int CPWV, int WPG, bool MID = false>
+__global__ void __launch_bounds__(64 * WPG * (MID ? 2 : 1)) Exl3GemmPrefillKernel(GemmArgs g) {
+  static_assert(!MID || 32 * WPG * CPWV == 128, "the fused mid needs one 128-column block per workgroup");
+  constexpr int NP = MID ? 2 : 1;       // planes per workgroup
   constexpr int T = TileDwords(K2);
   constexpr int SD = 4 * T;
   constexpr int DPL = (SD + 63) / 64;
@@ -376,25 +417,27 @@ __global__ void __launch_bounds__(64 * WPG) Exl3GemmPrefillKernel(GemmArgs g) {
   // Halves per staged activation row: 32 + 16 pad.  Measured LDS bank-conflict cycles of
   // the config-4 gate/up launch: 10.6 M at 48 against 24.4 M at 40, 56 or 72.
   constexpr int XS = 48;
-  constexpr int NT = 64 * WPG;             // threads
+  constexpr int NT = 64 * WPG;             // threads per plane
   constexpr int XL = (R * 4 + NT - 1) / NT;  // 16-byte activation loads per thread per step
   // The epilogue stages 16-row slabs (8.4 KB), so the activation tiles set the LDS size and
   // more workgroups fit a CU.
   constexpr int ER = 16;
   constexpr int NXB = 4;  // activation tile buffers (written for s + 1, read by the MFMAs of s - 1)
-  constexpr int XBYTES = NXB * R * XS * 2, EBYTES = ER * 132 * 4;
-  __shared__ uint32_t stage[WPG][CPWV][StageDwords<DPL>()];
+  constexpr int XBYTES = NP * NXB * R * XS * 2, EBYTES = NP * ER * 132 * 4;
+  __shared__ uint32_t stage[NP * WPG][CPWV][StageDwords<DPL>()];
   // Activation tiles during the main loop; the epilogue's row staging afterwards.
   __shared__ __align__(16) char smem[XBYTES > EBYTES ? XBYTES : EBYTES];
-  __half(*xs)[R][XS] = reinterpret_cast<__half(*)[R][XS]>(smem);
   const int n_entries = g.n_entries ? *g.n_entries : g.n_entries_host;
   const GridPos gp = XcdEntryMajor();
   const int ei = gp.y + g.entry_base;
   if (ei >= n_entries) return;
   const int4 ent = EntryOf(g, ei);
-  const GemmPlane& pl = g.plane[gp.z];
   const int cpg = gp.x;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int plane = MID ? wave / WPG : 0, lw = MID ? wave % WPG : wave;  // plane, wave within it
+  const int tp = (int)threadIdx.x - plane * NT;                            // thread within the plane
+  const GemmPlane& pl = g.plane[MID ? plane : gp.z];
+  __half(*xs)[R][XS] = reinterpret_cast<__half(*)[R][XS]>(smem + plane * (XBYTES / NP));
   const int steps = g.A / 2;
   const int row0 = ent.y, nrows = ent.z;
   const int nrb = (nrows + 15) / 16;
@@ -404,7 +447,7 @@ __global__ void __launch_bounds__(64 * WPG) Exl3GemmPrefillKernel(GemmArgs g) {
   __amdgpu_buffer_rsrc_t rw[CPWV];
 #pragma unroll
   for (int c = 0; c < CPWV; ++c) {
-    const int cp = (cpg * WPG + wave) * CPWV + c;
+    const int cp = (cpg * WPG + lw) * CPWV + c;
     rw[c] = MakeRsrc(m.tiles + (size_t)cp * g.A * 2 * T, (uint32_t)steps * SD * 4);
   }
   uint32_t woff[2][ND];
@@ -419,8 +462,8 @@ __global__ void __launch_bounds__(64 * WPG) Exl3GemmPrefillKernel(GemmArgs g) {
   uint32_t xoff[XL];
 #pragma unroll
   for (int i = 0; i < XL; ++i) {
-    const int row = (int)threadIdx.x / 4 + (NT / 4) * i;
-    xoff[i] = (uint32_t)((row * pl.ldx + 8 * (threadIdx.x & 3)) * 2);
+    const int row = tp / 4 + (NT / 4) * i;
+    xoff[i] = (uint32_t)((row * pl.ldx + 8 * (tp & 3)) * 2);
   }
   auto load_x = [&](u32x4_t (&xv)[XL], int s) {
 #pragma unroll
@@ -429,9 +472,9 @@ __global__ void __launch_bounds__(64 * WPG) Exl3GemmPrefillKernel(GemmArgs g) {
   auto store_x = [&](const u32x4_t (&xv)[XL], int buf) {
 #pragma unroll
     for (int i = 0; i < XL; ++i) {
-      const int row = (int)threadIdx.x / 4 + (NT / 4) * i;
+      const int row = tp / 4 + (NT / 4) * i;
       if ((NT / 4) * (i + 1) <= R || row < R)  // statically true when the loads cover R rows exactly
-        *reinterpret_cast<u32x4_t*>(&xs[buf][row][8 * (threadIdx.x & 3)]) = xv[i];
+        *reinterpret_cast<u32x4_t*>(&xs[buf][row][8 * (tp & 3)]) = xv[i];
     }
   };
 
@@ -459,7 +502,7 @@ __global__ void __launch_bounds__(64 * WPG) Exl3GemmPrefillKernel(GemmArgs g) {
   load_x(xq[0], PFX);
   // The MFMAs issued at step 0 (for the step before the first) read tile buffer NXB - 1
   // with zero fragments: zero it so they add exact zeros.
-  for (int i = threadIdx.x; i < R * XS / 8; i += NT)
+  for (int i = tp; i < R * XS / 8; i += NT)
     reinterpret_cast<u32x4_t*>(&xs[NXB - 1][0][0])[i] = u32x4_t{0u, 0u, 0u, 0u};
   __syncthreads();
 
@@ -556,6 +599,42 @@ __global__ void __launch_bounds__(64 * WPG) Exl3GemmPrefillKernel(GemmArgs g) {
     (void)((na == Is + 1 ? (main_loop(integral_constant<int, Is + 1>{}), true) : false) || ...);
   }(std::make_integer_sequence<int, NRBT>{});
 
+  if constexpr (MID) {
+    // Mid per 16-row slab: both planes' raw sums staged in LDS, then one row's block per
+    // 16 lanes of the first 16 ER threads.
+    float(*eb)[ER][132] = reinterpret_cast<float(*)[ER][132]>(smem);
+    const MatPtr mg = MatOf(g, g.plane[0], ent.x), mu = MatOf(g, g.plane[1], ent.x);
+    const int j = threadIdx.x & 15, c0 = cpg * 128 + 8 * j;
+    const int O = g.ncp * 32;
+    for (int r0 = 0; r0 < nrows; r0 += ER) {
+#pragma unroll
+      for (int i = 0; i < NRBT; ++i) {
+        if (i * 16 < r0 || i * 16 >= r0 + ER) continue;
+        const int cl = lw * 32 + ((lane & 15) >> 3) * 16 + (lane & 7);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = i * 16 - r0 + 4 * (lane >> 4) + e;
+          eb[plane][r][cl] = acc[i][0][0][e];
+          eb[plane][r][cl + 8] = acc[i][0][1][e];
+        }
+      }
+      __syncthreads();
+      const int rr = threadIdx.x >> 4;
+      if (rr < ER && r0 + rr < nrows) {
+        float gv[8], uv[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          gv[e] = eb[0][rr][8 * j + e];
+          uv[e] = eb[1][rr][8 * j + e];
+        }
+        const size_t p = (size_t)(row0 + r0 + rr);
+        MidBlock(gv, uv, mg.svh + c0, mu.svh + c0, g.mid_suh + (size_t)ent.x * O + c0,
+                 g.mid_xd + p * O + cpg * 128);
+      }
+      __syncthreads();
+    }
+    return;
+  }
   if (pl.epi >= 1) {
     // Output transform per 128-column block: stage y_h rows in LDS, ER rows at a time
     // (reusing the activation tile area), WHT128 * norm * svh per row.

@@ -13,7 +13,8 @@ namespace cx {
 #define CX_CAT2(a, b) a##b
 #define CX_CAT(a, b) CX_CAT2(a, b)
 
-bool CX_CAT(LaunchGemmPrefillRate, CX_RATE)(int cb, int nrbt, int wpg, dim3 grid, const GemmArgs& g, hipStream_t s) {
+bool CX_CAT(LaunchGemmPrefillRate, CX_RATE)(int cb, int nrbt, int wpg, bool mid, dim3 grid, const GemmArgs& g,
+                                           hipStream_t s) {
   constexpr int K2 = CX_RATE;
   auto go = [&](auto cbc, auto nc, auto wc) {
     constexpr int CB = decltype(cbc)::value, NRBT = decltype(nc)::value, WPG = decltype(wc)::value;
@@ -21,6 +22,11 @@ bool CX_CAT(LaunchGemmPrefillRate, CX_RATE)(int cb, int nrbt, int wpg, dim3 grid
     return true;
   };
   auto shape = [&](auto cbc) {
+    if (mid) {  // gate and up in one workgroup, the mid in the epilogue
+      if (nrbt != 4 || wpg != 4) return false;
+      hipLaunchKernelGGL((Exl3GemmPrefillKernel<K2, decltype(cbc)::value, 4, 1, 4, true>), grid, dim3(512), 0, s, g);
+      return true;
+    }
     if (nrbt == 4 && wpg == 4) return go(cbc, IC<4>{}, IC<4>{});
     if (nrbt == 4 && wpg == 8) return go(cbc, IC<4>{}, IC<8>{});
     if (nrbt == 4 && wpg == 16) return go(cbc, IC<4>{}, IC<16>{});

@@ -91,8 +91,9 @@ size_t LinearWorkspace(const LinearPlan& p, int I, int O, int M);
 // Launches Exl3GemmKernel for a runtime (rate, codebook, rows per wave, waves per
 // column pair).  Returns false for an unsupported combination.
 bool LaunchGemm(int k2, int cb, int nrb, int ksw, int u, dim3 grid, const GemmArgs& g, hipStream_t s);
-// The prefill GEMM (Exl3GemmPrefillKernel): grid (O / (32 wpg), entries padded to 8, planes).
-bool LaunchGemmPrefill(int k2, int cb, int nrbt, int wpg, dim3 grid, const GemmArgs& g, hipStream_t s);
+// The prefill GEMM (Exl3GemmPrefillKernel): grid (O / (32 wpg), entries padded to 8, planes);
+// mid: gate and up in one workgroup with the mid fused (grid (O / 128, entries padded, 1)).
+bool LaunchGemmPrefill(int k2, int cb, int nrbt, int wpg, bool mid, dim3 grid, const GemmArgs& g, hipStream_t s);
 // The tall prefill GEMM (Exl3GemmTallKernel): entries of up to 64 kTallRowBlocksPerWave
 // rows, grid (O / 128, entries padded to 8, planes).
 constexpr int kTallRowBlocksPerWave = 3;
@@ -100,7 +101,8 @@ bool LaunchGemmTall(int k2, int cb, dim3 grid, const GemmArgs& g, hipStream_t s)
 // Per-rate launchers (one translation unit per rate, gemm_inst.hip).
 #define CX_DECLARE_RATE(K2)                                                                          \
   bool LaunchGemmRate##K2(int cb, int nrb, int ksw, dim3 grid, const GemmArgs& g, hipStream_t s); \
-  bool LaunchGemmPrefillRate##K2(int cb, int nrbt, int wpg, dim3 grid, const GemmArgs& g, hipStream_t s); \
+  bool LaunchGemmPrefillRate##K2(int cb, int nrbt, int wpg, bool mid, dim3 grid, const GemmArgs& g, \
+                                 hipStream_t s);                                                         \
   bool LaunchGemmTallRate##K2(int cb, dim3 grid, const GemmArgs& g, hipStream_t s);
 CX_DECLARE_RATE(2)
 CX_DECLARE_RATE(3)

@@ -491,29 +491,10 @@ __global__ void __launch_bounds__(256) MoeMidKernel(const float* __restrict__ yg
   const int g = (threadIdx.x >> 4) & 3, j = threadIdx.x & 15;
   for (int blk = g; blk < I / 128; blk += 4) {
     const int c0 = blk * 128 + 8 * j;
-    float gv[8], uv[8], svg[8], svu[8], sud[8];
+    float gv[8], uv[8];
     LoadF8(yg + (size_t)p * I + c0, gv);
     LoadF8(yu + (size_t)p * I + c0, uv);
-    LoadH8(svg_p + c0, svg);
-    LoadH8(svu_p + c0, svu);
-    LoadH8(sud_p + c0, sud);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      gv[i] = 0.f + gv[i];
-      uv[i] = 0.f + uv[i];
-    }
-    Wht128x8Signed(gv);
-    Wht128x8Signed(uv);
-    const float sg = WhtLaneSign();
-    float v[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float a = gv[i] * (sg * (kHadNorm * svg[i]));
-      const float b = uv[i] * (sg * (kHadNorm * svu[i]));
-      v[i] = RoundH(RoundH(SiLU(a) * b) * sud[i]);
-    }
-    Wht128x8Signed(v);
-    StorePerm32x8(xd + (size_t)p * I + blk * 128, v, kHadNorm * sg);
+    MidBlock(gv, uv, svg_p + c0, svu_p + c0, sud_p + c0, xd + (size_t)p * I + blk * 128);
   }
 }
 
@@ -595,7 +576,7 @@ namespace cx {
 
 struct MoeSizes {
   int M, P, n, nsh, chunk, nrb, wpg, max_entries, ntiles;
-  bool small, prefill, tall;
+  bool small, prefill, tall, mid;
   size_t off_sel, off_wts, off_counts, off_offsets, off_pairs, off_rows, off_inv, off_rexp, off_ent, off_nent, off_tiles;
   size_t off_xg, off_xu, off_yg, off_yu, off_xd, off_yd, off_ysc, total;
 };
@@ -607,6 +588,7 @@ struct MoeSizes {
 struct PrefillShape {
   int nrb, wpg;
   int kernel;  // prefill GEMM: 0 register-blocked, 1 tall, -1 by the rows per expert
+  int mid;     // register-blocked prefill: mid fused into the gate/up GEMM
 };
 PrefillShape PrefillConfig() {
   static const PrefillShape ps = [] {
@@ -616,7 +598,8 @@ PrefillShape PrefillConfig() {
     };
     const int nrb = env("CX_PREFILL_NRB", 4) == 8 ? 8 : 4;
     const int w = env("CX_PREFILL_WPG", 4);
-    return PrefillShape{nrb, w == 16 && nrb == 4 ? 16 : w == 4 ? 4 : 8, env("CX_PREFILL_GEMM", -1)};
+    return PrefillShape{nrb, w == 16 && nrb == 4 ? 16 : w == 4 ? 4 : 8, env("CX_PREFILL_GEMM", -1),
+                        env("CX_PREFILL_MID", 1)};
   }();
   return ps;
 }
@@ -636,6 +619,9 @@ MoeSizes PlanMoe(const cx_moe_plan* pl, int M, int mode) {
   const int kern = ps.kernel >= 0 ? ps.kernel : (long)M * pl->topk >= 96L * pl->E ? 1 : 0;
   s.tall = !decode && kern == 1;
   if (s.tall) s.nrb = 4 * kTallRowBlocksPerWave;
+  // Register-blocked prefill: gate and up in one workgroup with the mid fused into the
+  // epilogue (64-row entries, 4 waves per plane).
+  s.mid = !decode && !s.tall && s.nrb == 4 && ps.mid;
   // Decode: one 16-row block per entry; prefill: every row of an entry shares each decoded tile.
   s.chunk = 16 * s.nrb;
   s.nsh = (M + s.chunk - 1) / s.chunk;
@@ -727,9 +713,11 @@ int LaunchGroup(const int* sel, GroupOut& o, int* tile_counts, int ntiles, hipSt
 // entries [nsh, n_entries).  Routed and shared matrices with different rates go in
 // separate launches.
 bool LaunchExpertGemm(const cx_moe_plan* pl, const MoeSizes& sz, bool gate_up, const __half* xa, const __half* xb,
-                      float* ya, float* yb, float* ysc, const int4* ent, const int* nent, const int* xmap,
+                      float* ya, float* yb, float* ysc, __half* xd, const int4* ent, const int* nent, const int* xmap,
                       hipStream_t s) {
   GemmArgs g{};
+  g.mid_suh = pl->tb.down_suh;
+  g.mid_xd = xd;
   g.xmap = xmap;
   g.xmap_n = sz.n;
   const int in = gate_up ? pl->H : pl->I, out = gate_up ? pl->I : pl->H;
@@ -753,11 +741,13 @@ bool LaunchExpertGemm(const cx_moe_plan* pl, const MoeSizes& sz, bool gate_up, c
   const int k2r = gate_up ? pl->k2_gu : pl->k2_d, cbr = gate_up ? pl->cb_gu : pl->cb_d;
   const int k2s = gate_up ? pl->k2_sgu : pl->k2_sd, cbs = gate_up ? pl->cb_sgu : pl->cb_sd;
   const int wpg = g.ncp % sz.wpg == 0 ? sz.wpg : 4;
-  const int cpg = sz.tall ? g.ncp / 4 : sz.prefill ? g.ncp / wpg : g.ncp / (4 / ksw);
+  const bool mid = gate_up && sz.mid;  // both planes in one workgroup, the mid fused
+  const int cpg = sz.tall ? g.ncp / 4 : mid ? g.ncp / 4 : sz.prefill ? g.ncp / wpg : g.ncp / (4 / ksw);
   auto launch = [&](int k2, int cb, int ny) {
     if (sz.tall) return LaunchGemmTall(k2, cb, dim3(cpg, (ny + 7) / 8 * 8, planes), g, s);
     if (sz.prefill)  // entry-major XCD placement needs the entry count padded to 8
-      return LaunchGemmPrefill(k2, cb, sz.nrb, wpg, dim3(cpg, (ny + 7) / 8 * 8, planes), g, s);
+      return LaunchGemmPrefill(k2, cb, sz.nrb, mid ? 4 : wpg, mid, dim3(cpg, (ny + 7) / 8 * 8, mid ? 1 : planes), g,
+                               s);
     return LaunchGemm(k2, cb, sz.nrb, ksw, 4, dim3(cpg, ny, planes), g, s);
   };
   if (k2r == k2s && cbr == cbs) {
@@ -993,15 +983,15 @@ int MoeForward(const cx_moe_plan* pl, const void* x, int32_t x_dtype, int32_t ld
                        xg, xu);
   }
   mark();
-  if (!LaunchExpertGemm(pl, sz, true, xg, xu, yg, yu, nullptr, ent, nent, front ? pairs : nullptr, s))
+  if (!LaunchExpertGemm(pl, sz, true, xg, xu, yg, yu, nullptr, xd, ent, nent, front ? pairs : nullptr, s))
     return CX_E_UNSUPPORTED;
   mark();
-  {
+  if (!sz.mid)  // else the gate/up GEMM wrote the down projection's input rows itself
     hipLaunchKernelGGL(MoeMidKernel, dim3((unsigned)((sz.P + 3) / 4)), dim3(256), 0, s, yg, yu, rexp,
                        pl->tb, M, pl->topk, pl->E, pl->I, xd);
-  }
   mark();
-  if (!LaunchExpertGemm(pl, sz, false, xd, nullptr, yd, nullptr, ysc, ent, nent, nullptr, s)) return CX_E_UNSUPPORTED;
+  if (!LaunchExpertGemm(pl, sz, false, xd, nullptr, yd, nullptr, ysc, nullptr, ent, nent, nullptr, s))
+    return CX_E_UNSUPPORTED;
   mark();
   {
     const long items = (long)M * (pl->H / 4);
