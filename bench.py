@@ -55,6 +55,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-linear", action="store_true", help="skip the config-2 ragged linear measurement")
     ap.add_argument("--no-long", action="store_true", help="skip the config-5 long prefill + output head")
+    ap.add_argument("--no-r1", action="store_true", help="skip the R = 1 decode latency measurement")
     ap.add_argument("--no-stream", action="store_true", help="skip the device-copy HBM stream measurement")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--min-warmup-s", type=float, default=0.5,
@@ -596,7 +597,8 @@ def main():
             "stage_us_mean": {n: round(float(stp[:, i].mean() * 1000), 2) for i, n in enumerate(
                 ["route", "group", "input", "gate_up", "mid", "down", "combine"])},
         }
-    out["decode_r1"] = bench_r1(plans, args.seed + 500)
+    if not args.no_r1:
+        out["decode_r1"] = bench_r1(plans, args.seed + 500)
     if not args.no_linear:
         out["linear"] = bench_linear(args.seed + 300)
     if not args.no_long:
