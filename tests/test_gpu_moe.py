@@ -156,6 +156,25 @@ def test_mixed_rates_layer(ops):
         assert rel_l2(y, ref) <= 1e-3
 
 
+@pytest.mark.parametrize("E,k,M,bgu,bd", [(8, 2, 500, 3, 5), (16, 4, 700, 4, 4), (4, 2, 300, 2, 8)])
+def test_tall_prefill_layer(ops, E, k, M, bgu, bd):
+    # At least 96 rows per expert on average selects the tall prefill GEMM: entries of up to
+    # 192 rows (one trellis decode for all of them), partial row blocks at their ends.
+    from exl3moe import synth
+    plan = synth.device_moe_layer(20 + E, E=E, H=256, Ie=256, topk=k, bits_gu=bgu, bits_d=bd)
+    rng = np.random.default_rng(M)
+    x = rng.standard_normal((M, 256)).astype(np.float16)
+    lg = rng.standard_normal((M, E + 1)).astype(np.float32)
+    y, sel, wts = run_layer(plan, x, lg, 2)
+    rs, rw = O.route(lg, E, k)
+    np.testing.assert_array_equal(sel, rs)
+    rows = np.sort(rng.choice(M, size=64, replace=False))
+    ref = oracle_layer(plan, x[rows], rs[rows], rw[rows])
+    e = rel_l2(y[rows], ref)
+    print(f"tall E={E} k={k} M={M} rel_l2={e:.3e}")
+    assert e <= 1e-3
+
+
 @pytest.fixture(scope="module")
 def layer512(ops):
     from exl3moe import synth
