@@ -513,6 +513,11 @@ struct HcArgs {
 // block (F16, prefill: the reference's prefill keeps d_k in fp16 too,
 // engine/layers/prefill_moe.h:648).  engine/layers/moe_rows.h:634-682.  HC: accumulate
 // into the residual streams instead of storing y (engine/layers/moe_rows.h:672-681).
+// One combine weight step: acc + w * d with one rounding.
+__device__ __forceinline__ float CombineStep(float acc, float w, float d) { return __builtin_fmaf(w, d, acc); }
+// topk below this: every slot's row and weight are loaded at once (unrolled).
+constexpr int kCombineSlots = 16;
+
 template <bool HC, bool F16>
 __global__ void __launch_bounds__(256) MoeCombineKernel(const void* __restrict__ pd, const float* __restrict__ psc,
                                                         const float* __restrict__ wts, const int* __restrict__ inv,
@@ -521,34 +526,53 @@ __global__ void __launch_bounds__(256) MoeCombineKernel(const void* __restrict__
   const int item = blockIdx.x * blockDim.x + threadIdx.x;
   if (item >= M * nq) return;
   const int r = item / nq, c0 = (item % nq) * 4;
-  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll 4
-  for (int k = 0; k <= topk; ++k) {
-    const int p = k < topk ? inv[r * topk + k] : M * topk + r;
-    float4 d;
+  auto slot_row = [&](int k) { return k < topk ? inv[r * topk + k] : M * topk + r; };
+  auto load = [&](int p) {
     if constexpr (F16) {
       const uint2 u = *reinterpret_cast<const uint2*>(static_cast<const __half*>(pd) + (size_t)p * H + c0);
       const float sc = psc[(size_t)p * (H / 128) + c0 / 128];
       const float2 a = __half22float2(__builtin_bit_cast(__half2, u.x)), b = __half22float2(__builtin_bit_cast(__half2, u.y));
-      d = make_float4(a.x * sc, a.y * sc, b.x * sc, b.y * sc);
+      return make_float4(a.x * sc, a.y * sc, b.x * sc, b.y * sc);
     } else {
-      d = *reinterpret_cast<const float4*>(static_cast<const float*>(pd) + (size_t)p * H + c0);
+      return *reinterpret_cast<const float4*>(static_cast<const float*>(pd) + (size_t)p * H + c0);
     }
-    const float w = wts[(size_t)r * (topk + 1) + k];
-    acc.x += w * d.x;
-    acc.y += w * d.y;
-    acc.z += w * d.z;
-    acc.w += w * d.w;
+  };
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  auto add = [&](float w, float4 d) {
+    acc.x = CombineStep(acc.x, w, d.x);
+    acc.y = CombineStep(acc.y, w, d.y);
+    acc.z = CombineStep(acc.z, w, d.z);
+    acc.w = CombineStep(acc.w, w, d.w);
+  };
+  if (topk < kCombineSlots) {
+    // All slot rows, then all their loads, issued before the first use (the rows and
+    // weights of slots past topk repeat the last slot and are not added): one memory
+    // latency per stage instead of one per slot.
+    int p[kCombineSlots];
+    float w[kCombineSlots];
+    float4 d[kCombineSlots];
+#pragma unroll
+    for (int k = 0; k < kCombineSlots; ++k) {
+      p[k] = slot_row(min(k, topk));
+      w[k] = wts[(size_t)r * (topk + 1) + min(k, topk)];
+    }
+#pragma unroll
+    for (int k = 0; k < kCombineSlots; ++k) d[k] = load(p[k]);
+#pragma unroll
+    for (int k = 0; k < kCombineSlots; ++k)
+      if (k <= topk) add(w[k], d[k]);
+  } else {
+    for (int k = 0; k <= topk; ++k) add(wts[(size_t)r * (topk + 1) + k], load(slot_row(k)));
   }
   if constexpr (HC) {
     for (int st = 0; st < hc.n_streams; ++st) {
       const float g = hc.post[(size_t)r * hc.n_streams + st];
       float4* h = reinterpret_cast<float4*>(hc.H + (size_t)r * hc.ldh + (size_t)st * H + c0);
       float4 v = *h;
-      v.x += g * acc.x;
-      v.y += g * acc.y;
-      v.z += g * acc.z;
-      v.w += g * acc.w;
+      v.x = CombineStep(v.x, g, acc.x);
+      v.y = CombineStep(v.y, g, acc.y);
+      v.z = CombineStep(v.z, g, acc.z);
+      v.w = CombineStep(v.w, g, acc.w);
       *h = v;
     }
   } else {
