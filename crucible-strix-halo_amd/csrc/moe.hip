@@ -507,17 +507,17 @@ struct HcArgs {
   int n_streams;
 };
 
+// One combine weight step: acc + w * d with one rounding.
+__device__ __forceinline__ float CombineStep(float acc, float w, float d) { return __builtin_fmaf(w, d, acc); }
+// topk below this: every slot's row and weight are loaded at once (unrolled).
+constexpr int kCombineSlots = 16;
+
 // Combine: per row, slots 0..topk-1 in selection order then the shared expert:
 // y += w_k * d_k, fp32, where d_k = WHT(y_h) * (norm * svh) came out of the down GEMM's
 // epilogue: fp32 rows (decode), or fp16 rows with a power-of-two scale per 128-column
 // block (F16, prefill: the reference's prefill keeps d_k in fp16 too,
 // engine/layers/prefill_moe.h:648).  engine/layers/moe_rows.h:634-682.  HC: accumulate
 // into the residual streams instead of storing y (engine/layers/moe_rows.h:672-681).
-// One combine weight step: acc + w * d with one rounding.
-__device__ __forceinline__ float CombineStep(float acc, float w, float d) { return __builtin_fmaf(w, d, acc); }
-// topk below this: every slot's row and weight are loaded at once (unrolled).
-constexpr int kCombineSlots = 16;
-
 template <bool HC, bool F16>
 __global__ void __launch_bounds__(256) MoeCombineKernel(const void* __restrict__ pd, const float* __restrict__ psc,
                                                         const float* __restrict__ wts, const int* __restrict__ inv,
