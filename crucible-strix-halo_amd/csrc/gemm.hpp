@@ -28,21 +28,29 @@
 
 namespace cx {
 
-// Per-wave LDS staging of one step: dword d of the step lives at d + 2 (d / 32), so the
-// two column tiles of a step (T = 8K dwords apart) do not map their equal dword
-// offsets onto one bank, and 8-byte lane slices stay 8-byte aligned.
-__host__ __device__ constexpr int StagePad(int d) { return d + 2 * (d / 32); }
-template <int DPL>
-__host__ __device__ constexpr int StageDwords() { return StagePad(64 * DPL) + 2; }
-// Writes a lane's DPL dwords of a step into the padded staging slot.  Slices of 1, 2
-// or 4 dwords never straddle a 32-dword boundary; 3-dword slices are written one by one.
-template <int DPL>
+// Per-wave LDS staging of one step.  At most rates dword d of the step lives at
+// d + 2 (d / 32), so the two column tiles of a step (T = 8K dwords apart) do not map their
+// equal dword offsets onto one bank, and 8-byte lane slices stay 8-byte aligned.  At
+// K2 = 6, 10 and 12 (3, 5, 6 bpw) the windows of a half wave spread over the banks better
+// without padding: a model of the 32-bank mapping of the window reads and staging writes
+// gives 4 / 12 / 12 extra cycles per step unpadded against 8 / 36 / 36 padded (the measured
+// conflict cycles per LDS instruction of the 6-bpw decode GEMM were 3.9 padded), and the
+// same count as now (0 at 4 bpw) at every other rate.
+template <int K2>
+__host__ __device__ constexpr int StagePad(int d) {
+  return K2 == 6 || K2 == 10 || K2 == 12 ? d : d + 2 * (d / 32);
+}
+template <int K2, int DPL>
+__host__ __device__ constexpr int StageDwords() { return StagePad<K2>(64 * DPL) + 2; }
+// Writes a lane's DPL dwords of a step into the staging slot.  Slices of 1, 2 or 4 dwords
+// never straddle a 32-dword boundary; 3-dword slices are written one by one.
+template <int K2, int DPL>
 __device__ __forceinline__ void StageWrite(uint32_t* slot, int lane, const uint32_t* v) {
   if constexpr (DPL == 3) {
 #pragma unroll
-    for (int i = 0; i < 3; ++i) slot[StagePad(3 * lane + i)] = v[i];
+    for (int i = 0; i < 3; ++i) slot[StagePad<K2>(3 * lane + i)] = v[i];
   } else {
-    const int o = StagePad(lane * DPL);
+    const int o = StagePad<K2>(lane * DPL);
 #pragma unroll
     for (int i = 0; i < DPL; ++i) slot[o + i] = v[i];
   }
@@ -193,7 +201,7 @@ __device__ __forceinline__ void StreamColumnPair(const uint32_t* tiles, int step
 #pragma unroll
   for (int j = 0; j < 2; ++j)
 #pragma unroll
-    for (int i = 0; i < ND; ++i) woff[j][i] = (uint32_t)StagePad((2 * j + lr.tile) * T + (lr.d0 + i) % T);
+    for (int i = 0; i < ND; ++i) woff[j][i] = (uint32_t)StagePad<K2>((2 * j + lr.tile) * T + (lr.d0 + i) % T);
   const uint32_t loff = (uint32_t)lane * DPL * 4;
   uint32_t xoff[NRB];
 #pragma unroll
@@ -207,7 +215,7 @@ __device__ __forceinline__ void StreamColumnPair(const uint32_t* tiles, int step
   auto step = [&](const Dwords<DPL>& w, const u32x4_t (&xv)[NRB]) {
     // Stage the step in the wave's slot; LDS executes a wave's operations in order, so
     // the window reads below see these writes and the next step's writes follow them.
-    StageWrite<DPL>(slot, lane, w.v);
+    StageWrite<K2, DPL>(slot, lane, w.v);
     __builtin_amdgcn_wave_barrier();
     uint32_t v[2][3];
 #pragma unroll
@@ -268,7 +276,7 @@ Exl3GemmKernel(GemmArgs g) {
   constexpr int CPW = 4 / KSW;
   constexpr int T = TileDwords(K2);
   constexpr int DPL = (4 * T + 63) / 64;
-  __shared__ uint32_t stage[4][StageDwords<DPL>()];
+  __shared__ uint32_t stage[4][StageDwords<K2, DPL>()];
   // Device tables: entries past the last real one have 0 rows (the grid never exceeds the
   // table), so a wave's first weight load waits on two dependent scalar loads (entry,
   // matrix pointers) and no entry count.
@@ -424,7 +432,7 @@ __global__ void __launch_bounds__(64 * WPG * (MID ? 2 : 1)) Exl3GemmPrefillKerne
   constexpr int ER = 16;
   constexpr int NXB = 4;  // activation tile buffers (written for s + 1, read by the MFMAs of s - 1)
   constexpr int XBYTES = NP * NXB * R * XS * 2, EBYTES = NP * ER * 132 * 4;
-  __shared__ uint32_t stage[NP * WPG][CPWV][StageDwords<DPL>()];
+  __shared__ uint32_t stage[NP * WPG][CPWV][StageDwords<K2, DPL>()];
   // Activation tiles during the main loop; the epilogue's row staging afterwards.
   __shared__ __align__(16) char smem[XBYTES > EBYTES ? XBYTES : EBYTES];
   const int n_entries = g.n_entries ? *g.n_entries : g.n_entries_host;
@@ -454,7 +462,7 @@ __global__ void __launch_bounds__(64 * WPG * (MID ? 2 : 1)) Exl3GemmPrefillKerne
 #pragma unroll
   for (int j = 0; j < 2; ++j)
 #pragma unroll
-    for (int i = 0; i < ND; ++i) woff[j][i] = (uint32_t)StagePad((2 * j + lr.tile) * T + (lr.d0 + i) % T);
+    for (int i = 0; i < ND; ++i) woff[j][i] = (uint32_t)StagePad<K2>((2 * j + lr.tile) * T + (lr.d0 + i) % T);
   const uint32_t loff = (uint32_t)lane * DPL * 4;
 
   // Activation tile loads: thread t moves rows t / 4 + 64 i, quarter t % 4 (16 bytes).
@@ -552,7 +560,7 @@ __global__ void __launch_bounds__(64 * WPG * (MID ? 2 : 1)) Exl3GemmPrefillKerne
         half8_t b[CPWV][2];
 #pragma unroll
         for (int c = 0; c < CPWV; ++c) {
-          StageWrite<DPL>(slot[c], lane, wq[qw][c].v);
+          StageWrite<K2, DPL>(slot[c], lane, wq[qw][c].v);
           __builtin_amdgcn_wave_barrier();
           uint32_t v[2][3];
 #pragma unroll
@@ -725,7 +733,7 @@ Exl3GemmTallKernel(GemmArgs g) {
   constexpr int ER = 16;                       // epilogue slab rows (one row block)
   constexpr int BBYTES = 2 * 4 * 2 * 64 * 16;  // [buffer][column pair][fragment][lane] x 16 B
   constexpr int EBYTES = 4 * ER * 132 * 4;     // one slab per wave
-  __shared__ uint32_t stage[4][StageDwords<DPL>()];
+  __shared__ uint32_t stage[4][StageDwords<K2, DPL>()];
   __shared__ __align__(16) char smem[BBYTES > EBYTES ? BBYTES : EBYTES];
   u32x4_t* bs = reinterpret_cast<u32x4_t*>(smem);
   const int n_entries = g.n_entries ? *g.n_entries : g.n_entries_host;
@@ -748,7 +756,7 @@ Exl3GemmTallKernel(GemmArgs g) {
 #pragma unroll
   for (int j = 0; j < 2; ++j)
 #pragma unroll
-    for (int i = 0; i < ND; ++i) woff[j][i] = (uint32_t)StagePad((2 * j + lr.tile) * T + (lr.d0 + i) % T);
+    for (int i = 0; i < ND; ++i) woff[j][i] = (uint32_t)StagePad<K2>((2 * j + lr.tile) * T + (lr.d0 + i) % T);
   const uint32_t loff = (uint32_t)lane * DPL * 4;
   uint32_t* slot = stage[wave];
   // Activations: rows past the entry lie outside the buffer resource and read as zeros.
@@ -756,7 +764,7 @@ Exl3GemmTallKernel(GemmArgs g) {
 
   // A step's weights go through the wave's LDS slot: staged (written) one step before its
   // decode, windows read back at the start of the decode's step.
-  auto stage_w = [&](const Dwords<DPL>& w) { StageWrite<DPL>(slot, lane, w.v); };
+  auto stage_w = [&](const Dwords<DPL>& w) { StageWrite<K2, DPL>(slot, lane, w.v); };
   auto read_windows = [&](uint32_t (&v)[2][3]) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {

@@ -15,7 +15,9 @@
         issue utilisation of the kernels whose name contains SUBSTR from one `--pmc` run with
         GRBM_GUI_ACTIVE, SQ_ACTIVE_INST_VALU, SQ_VALU_MFMA_BUSY_CYCLES and SQ_INSTS_MFMA:
         the fraction of SIMD cycles issuing VALU work and keeping the matrix cores busy,
-        and the MFMA issue rate in TFLOP/s against the dense fp16 peak.
+        and the MFMA issue rate in TFLOP/s against the dense fp16 peak; with SQ_INSTS_LDS
+        and SQ_LDS_BANK_CONFLICT (a second pass under the same DIR) the bank-conflict
+        cycles per LDS instruction.
 """
 from __future__ import annotations
 
@@ -100,6 +102,7 @@ def traffic(fetch_dir: str, write_dir: str, out: str, copy_bytes: int, kernel: s
 # MI355X (gfx950): 8 XCDs, 256 CUs x 4 SIMDs, 2.4 GHz peak engine clock, dense fp16 MFMA
 # peak 2.5 PFLOP/s; v_mfma_f32_16x16x32_f16 is 2 x 16 x 16 x 32 FLOP.
 XCDS, SIMDS, CLOCK_HZ, MFMA_PEAK_TFLOPS, MFMA_FLOP = 8, 1024, 2.4e9, 2500.0, 16384
+CUS = SIMDS // 4
 
 
 def counters(d: str, out: str, kernels: dict[str, str], cmd: str) -> dict:
@@ -140,6 +143,11 @@ def counters(d: str, out: str, kernels: dict[str, str], cmd: str) -> dict:
             tf = avg["SQ_INSTS_MFMA"] * MFMA_FLOP / (cycles / CLOCK_HZ) / 1e12
             k["mfma_issue_TFLOPs"] = round(tf, 1)
             k["mfma_issue_frac_of_peak"] = round(tf / MFMA_PEAK_TFLOPS, 4)
+        if "SQ_INSTS_LDS" in avg and "SQ_LDS_BANK_CONFLICT" in avg:
+            # Bank-conflict stall cycles (summed over the CUs) per LDS instruction issued,
+            # and as a share of all CU cycles of the launch.
+            k["lds_conflict_cycles_per_lds_instruction"] = round(avg["SQ_LDS_BANK_CONFLICT"] / max(1.0, avg["SQ_INSTS_LDS"]), 4)
+            k["lds_conflict_frac_of_cu_cycles"] = round(avg["SQ_LDS_BANK_CONFLICT"] / (cycles * CUS), 4)
         res["kernels"][label] = k
     with open(out, "w") as o:
         json.dump(res, o, indent=1)
