@@ -909,22 +909,31 @@ Exl3GemmTallKernel(GemmArgs g) {
       }
       return;
     }
+    // Raw sums: each row block (16 x 128 fp32) staged in the wave's slab and written as
+    // 16-byte pieces, 8 store instructions per lane instead of 32 single-float ones.
+    float(*eb)[132] = reinterpret_cast<float(*)[132]>(smem + wave * ER * 132 * 4);
 #pragma unroll
     for (int i = 0; i < NA; ++i) {
       const int rb = wave + 4 * i;
+      if (rb >= nrb) break;  // wave-uniform
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int col = (2 * (cpg * 4 + c) + ((lane & 15) >> 3)) * 16 + (lane & 7);
+      for (int c = 0; c < 4; ++c)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const int r = rb * 16 + 4 * (lane >> 4) + e;
-          if (r < nrows) {
-            float* yr = pl.y + (size_t)(row0 + r) * pl.ldy;
-            yr[col] = acc[i][c][0][e];
-            yr[col + 8] = acc[i][c][1][e];
-          }
+          const int cl = c * 32 + ((lane & 15) >> 3) * 16 + (lane & 7);
+          eb[4 * (lane >> 4) + e][cl] = acc[i][c][0][e];
+          eb[4 * (lane >> 4) + e][cl + 8] = acc[i][c][1][e];
         }
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int rr = 2 * k + (lane >> 5), c4 = 4 * (lane & 31);
+        const int r = rb * 16 + rr;
+        if (r < nrows)
+          *reinterpret_cast<float4*>(pl.y + (size_t)(row0 + r) * pl.ldy + cpg * 128 + c4) =
+              *reinterpret_cast<const float4*>(&eb[rr][c4]);
       }
+      __builtin_amdgcn_wave_barrier();
     }
   };
   using std::integral_constant;
