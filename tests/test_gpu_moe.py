@@ -213,8 +213,9 @@ def test_config3_decode(ops, layer512):
     assert np.abs(y - ref).max() <= 2e-3 * np.abs(ref).max()
 
 
-def test_config4_prefill_subset(ops, layer512):
-    # 2048 tokens with a Zipf(1.1) per-expert router bias; oracle on 48 sampled rows.
+def test_config4_prefill(ops, layer512):
+    # 2048 tokens with a Zipf(1.1) per-expert router bias; every row against the oracle
+    # (about 20 s of OpenMP oracle work on the GPU box's 16 host threads).
     from exl3moe import synth
     rng = np.random.default_rng(44)
     M = 2048
@@ -226,11 +227,15 @@ def test_config4_prefill_subset(ops, layer512):
     np.testing.assert_array_equal(sel, rs)
     counts = np.bincount(rs.ravel(), minlength=512)
     print(f"config4 expert counts: max={counts.max()} zero={np.sum(counts == 0)}")
-    rows = np.sort(rng.choice(M, size=48, replace=False))
-    ref = oracle_layer(layer512, x[rows], rs[rows], rw[rows])
-    e = rel_l2(y[rows], ref)
-    print(f"config4 rel_l2={e:.3e} max_abs={np.abs(y[rows] - ref).max():.3e}")
+    ref = oracle_layer(layer512, x, rs, rw)
+    e = rel_l2(y, ref)
+    print(f"config4 rel_l2={e:.3e} max_abs={np.abs(y - ref).max():.3e}")
     assert e <= 1e-3
+    assert np.abs(y - ref).max() <= 2e-3 * np.abs(ref).max()
+    # Row by row too: no single row far off while the whole passes.
+    per_row = np.sqrt(((y - ref) ** 2).sum(1) / (ref ** 2).sum(1))
+    print(f"config4 worst row rel_l2={per_row.max():.3e}")
+    assert per_row.max() <= 2e-3
     # Decode and prefill plans agree on the same rows: they sum K in different fp32 orders,
     # which the fp16 rounding points of the mid step can amplify to ~1e-4, and the prefill
     # keeps the down outputs in fp16 (one rounding, 2^-12 relative rms) as the reference's
@@ -310,9 +315,9 @@ def test_hc_errors(ops):
     assert e.value.rc == -2
 
 
-def test_config5_long_prefill_subset(ops):
+def test_config5_long_prefill(ops):
     # 8192 tokens through a 512-expert layer with gate/up at 3 bpw and down at 5 bpw
-    # (shared expert at the same rates); oracle on 32 sampled rows (rows are independent).
+    # (shared expert at the same rates); every row against the oracle.
     from exl3moe import synth
     plan = synth.device_moe_layer(5, E=512, H=2048, Ie=512, topk=10, bits_gu=3, bits_d=5)
     rng = np.random.default_rng(55)
@@ -322,18 +327,20 @@ def test_config5_long_prefill_subset(ops):
     y, sel, wts = run_layer(plan, x, lg, 2)
     rs, rw = O.route(lg, 512, 10)
     np.testing.assert_array_equal(sel, rs)
-    rows = np.sort(rng.choice(M, size=32, replace=False))
-    ref = oracle_layer(plan, x[rows], rs[rows], rw[rows])
-    e = rel_l2(y[rows], ref)
-    print(f"config5 rel_l2={e:.3e} max_abs={np.abs(y[rows] - ref).max():.3e}")
+    ref = oracle_layer(plan, x, rs, rw)
+    e = rel_l2(y, ref)
+    print(f"config5 rel_l2={e:.3e} max_abs={np.abs(y - ref).max():.3e}")
+    per_row = np.sqrt(((y - ref) ** 2).sum(1) / (ref ** 2).sum(1))
+    print(f"config5 worst row rel_l2={per_row.max():.3e}")
+    assert per_row.max() <= 2e-3
     assert e <= 1e-3
-    assert np.abs(y[rows] - ref).max() <= 2e-3 * np.abs(ref).max()
+    assert np.abs(y - ref).max() <= 2e-3 * np.abs(ref).max()
 
 
 def test_config5_output_head(ops):
     # EXL3 6-bpw head 2048 -> 151936 on the last token of 4 sessions; the output
-    # transform works per 128-column block, so column slices are checked against the
-    # oracle on the matching trellis / svh slices.
+    # transform works per 128-column block, so every column is checked against the oracle
+    # in chunks of 8192 columns (the matching trellis / svh slices).
     from exl3moe import synth
     rng = np.random.default_rng(56)
     tr, suh, svh = synth.linear(rng, 2048, 151936, 6)
@@ -341,10 +348,14 @@ def test_config5_output_head(ops):
     x = rng.standard_normal((4, 2048)).astype(np.float16)
     y = lin(torch.from_numpy(x).cuda(), row_offsets=[0, 1, 2, 3, 4]).cpu().numpy()
     assert np.all(np.isfinite(y))
-    for c0 in (0, 75904, 151936 - 256):
-        ts = np.ascontiguousarray(tr[:, c0 // 16:(c0 + 256) // 16])
-        ref = O.matvec(x, O.reconstruct_inner(ts, 6), suh, svh[c0:c0 + 256], np.float32)
-        assert rel_l2(y[:, c0:c0 + 256], ref) <= 1e-3
+    worst = 0.0
+    for c0 in range(0, 151936, 8192):
+        c1 = min(c0 + 8192, 151936)
+        ts = np.ascontiguousarray(tr[:, c0 // 16:c1 // 16])
+        ref = O.matvec(x, O.reconstruct_inner(ts, 6), suh, svh[c0:c1], np.float32)
+        worst = max(worst, rel_l2(y[:, c0:c1], ref))
+    print(f"head worst 8192-column chunk rel_l2={worst:.3e}")
+    assert worst <= 1e-3
 
 
 @pytest.mark.parametrize("mode", [1, 2])
