@@ -168,9 +168,8 @@ def test_tall_prefill_layer(ops, E, k, M, bgu, bd):
     y, sel, wts = run_layer(plan, x, lg, 2)
     rs, rw = O.route(lg, E, k)
     np.testing.assert_array_equal(sel, rs)
-    rows = np.sort(rng.choice(M, size=64, replace=False))
-    ref = oracle_layer(plan, x[rows], rs[rows], rw[rows])
-    e = rel_l2(y[rows], ref)
+    ref = oracle_layer(plan, x, rs, rw)
+    e = rel_l2(y, ref)
     print(f"tall E={E} k={k} M={M} rel_l2={e:.3e}")
     assert e <= 1e-3
 
@@ -475,7 +474,6 @@ def test_fp32_input(ops, layer512, mode):
     xh = xf.astype(np.float16)
     y16 = layer512(torch.from_numpy(xh).cuda(), lg, mode=mode).cpu().numpy()
     np.testing.assert_array_equal(y32.view(np.uint32), y16.view(np.uint32))
-    rows = np.arange(M) if mode == 1 else np.sort(rng.choice(M, size=24, replace=False))
     rs, rw = O.route(lgh, 512, 10)
-    ref = oracle_layer(layer512, xh[rows], rs[rows], rw[rows])
-    assert rel_l2(y32[rows], ref) <= 1e-3
+    ref = oracle_layer(layer512, xh, rs, rw)
+    assert rel_l2(y32, ref) <= 1e-3
