@@ -33,11 +33,9 @@ bool CX_CAT(LaunchGemmRate, CX_RATE)(int cb, int nrb, int ksw, dim3 grid, const 
     return false;
   };
   if (cb == kCbMul1) return split(IC<kCbMul1>{});
-  if constexpr (K2 % 2 == 0) {
-    // Legacy codebooks: one 16-row block per wave, K split inside the workgroup.
-    if (nrb != 1 || ksw != 4) return false;
-    if (cb == kCbMcg) return go(IC<kCbMcg>{}, IC<1>{}, IC<4>{});
-    if (cb == kCb3Inst) return go(IC<kCb3Inst>{}, IC<1>{}, IC<4>{});
+  if constexpr (K2 % 2 == 0) {  // the mcg and 3inst codebooks exist at whole bit rates only
+    if (cb == kCbMcg) return split(IC<kCbMcg>{});
+    if (cb == kCb3Inst) return split(IC<kCb3Inst>{});
   }
   return false;
 }

@@ -51,8 +51,10 @@ def device_linear(gen, I: int, O: int, bits: float, device="cuda", codebook: str
 
 
 def device_moe_layer(seed: int, E: int, H: int, Ie: int, topk: int, bits_gu: float = 4, bits_d: float = 4,
-                     shared_bits_gu: float | None = None, shared_bits_d: float | None = None, device="cuda"):
-    """Seeded synthetic MoE layer on the device: E routed experts plus the shared expert."""
+                     shared_bits_gu: float | None = None, shared_bits_d: float | None = None, device="cuda",
+                     codebook: str = "mul1"):
+    """Seeded synthetic MoE layer on the device: E routed experts plus the shared expert,
+    every matrix with the given codebook."""
     import torch
     from .ops import MoePlan
     gen = torch.Generator(device=device)
@@ -61,8 +63,9 @@ def device_moe_layer(seed: int, E: int, H: int, Ie: int, topk: int, bits_gu: flo
     sd = bits_d if shared_bits_d is None else shared_bits_d
 
     def one(bgu, bd):
-        return {"gate": device_linear(gen, H, Ie, bgu, device), "up": device_linear(gen, H, Ie, bgu, device),
-                "down": device_linear(gen, Ie, H, bd, device)}
+        return {"gate": device_linear(gen, H, Ie, bgu, device, codebook),
+                "up": device_linear(gen, H, Ie, bgu, device, codebook),
+                "down": device_linear(gen, Ie, H, bd, device, codebook)}
 
     experts = [one(bits_gu, bits_d) for _ in range(E)]
     shared = one(sg, sd)

@@ -119,6 +119,21 @@ def test_linear_other_rates(ops, bits):
     assert rel_l2(y, ref) <= 1e-3
 
 
+@pytest.mark.parametrize("bits,cb", [(4, "mcg"), (3, "3inst"), (2, "mcg"), (6, "3inst")])
+def test_linear_other_codebooks(ops, bits, cb):
+    # The mcg and 3inst codebooks through the decode GEMM (one and several row blocks).
+    from exl3moe import synth
+    rng = np.random.default_rng(int(bits * 10) + len(cb))
+    tr, suh, svh = synth.linear(rng, 512, 256, bits)
+    lin = ops.DeviceLinear.from_trellis(tr, suh, svh, bits, codebook=cb)
+    w = O.reconstruct_inner(tr, bits, cb)
+    for M in (5, 70):
+        x = rng.standard_normal((M, 512)).astype(np.float16)
+        y = lin(torch.from_numpy(x).cuda(), torch.float32).cpu().numpy()
+        ref = O.matvec(x, w, suh, svh, np.float32)
+        assert rel_l2(y, ref) <= 1e-3
+
+
 def test_rows_invariant_to_batch(ops):
     # A row's output is bitwise the same whatever other rows share the call.
     from exl3moe import synth

@@ -174,6 +174,24 @@ def test_tall_prefill_layer(ops, E, k, M, bgu, bd):
     assert e <= 1e-3
 
 
+@pytest.mark.parametrize("cb", ["mcg", "3inst"])
+def test_layer_other_codebooks(ops, cb):
+    # Every matrix of the layer in the mcg or 3inst codebook: decode, the register-blocked
+    # prefill GEMM (fused mid) and the tall prefill GEMM, against the oracle.
+    from exl3moe import synth
+    for E, k, M, mode in ((16, 4, 40, 1), (16, 4, 40, 2), (8, 2, 500, 2)):
+        plan = synth.device_moe_layer(70 + E, E=E, H=256, Ie=256, topk=k, codebook=cb)
+        rng = np.random.default_rng(M + mode)
+        x = rng.standard_normal((M, 256)).astype(np.float16)
+        lg = rng.standard_normal((M, E + 1)).astype(np.float32)
+        y, sel, wts = run_layer(plan, x, lg, mode)
+        rs, rw = O.route(lg, E, k)
+        np.testing.assert_array_equal(sel, rs)
+        e = rel_l2(y, oracle_layer(plan, x, rs, rw))
+        print(f"{cb} E={E} k={k} M={M} mode={mode} rel_l2={e:.3e}")
+        assert e <= 1e-3
+
+
 @pytest.fixture(scope="module")
 def layer512(ops):
     from exl3moe import synth
