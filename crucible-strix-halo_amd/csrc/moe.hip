@@ -57,7 +57,8 @@ __device__ __forceinline__ void SortLane(float (&v)[V], int (&id)[V]) {
 // l, l + 64, ... (E <= 64 V), sorted per lane once; each of the k rounds takes the wave
 // maximum of the lane heads, and the winning lane (the only one holding the max, or the
 // lowest id among equal maxima) pops its head.  NaN logits rank as -inf.
-// Writes sel_row[0..k), wts_row[0..k] and, if s_row is given, s_row[0..k) (LDS copy).
+// Writes sel_row[0..k), wts_row[0..k] (unless sel_row is null) and, if s_row is given,
+// s_row[0..k) (LDS copy).
 template <int V>
 __device__ __forceinline__ void RouteRowWave(const float* __restrict__ lg, int E, int topk, float shared,
                                              int* __restrict__ sel_row, float* __restrict__ wts_row, int* s_row) {
@@ -101,11 +102,13 @@ __device__ __forceinline__ void RouteRowWave(const float* __restrict__ lg, int E
   float sum = 0.f;
   for (int k = 0; k < topk; ++k) sum += __shfl(ex, k, 64);
   if (lane < topk) {
-    sel_row[lane] = myid;
-    wts_row[lane] = ex / sum;
+    if (sel_row) {
+      sel_row[lane] = myid;
+      wts_row[lane] = ex / sum;
+    }
     if (s_row) s_row[lane] = myid;
   }
-  if (lane == 0) wts_row[topk] = Sigmoid(shared);
+  if (lane == 0 && wts_row) wts_row[topk] = Sigmoid(shared);
 }
 
 // One wave per row.
@@ -322,6 +325,60 @@ __global__ void __launch_bounds__(1024) GroupInputKernel(const int* __restrict__
   const int wpr = (items + per - 1) / per;                    // workgroups per row
   const int row = (blockIdx.x - 1) / wpr, part = (blockIdx.x - 1) % wpr;
   if ((int)threadIdx.x <= topk) s_e[threadIdx.x] = (int)threadIdx.x < topk ? sel[(size_t)row * topk + threadIdx.x] : o.E;
+  __syncthreads();
+  const size_t xr = (size_t)row * ldx;
+  for (int it = part * per + (threadIdx.x >> 4); it < min(items, (part + 1) * per); it += per) {
+    const int slot = it / nb, blk = it % nb;
+    const int e = s_e[slot];
+    const size_t q = slot < topk ? (size_t)row * topk + slot : (size_t)M * topk + row;
+    const int c0 = blk * 128 + 8 * j;
+    float a[8], v[8];
+    InputPairTransform(LoadAsH8(x, xf32, xr + c0),
+                       *reinterpret_cast<const uint4*>(tb.gate_suh + (size_t)e * H + c0),
+                       *reinterpret_cast<const uint4*>(tb.up_suh + (size_t)e * H + c0), a, v);
+    StorePerm32x8(xg + q * H + blk * 128, a, kHadNorm * WhtLaneSign());
+    StorePerm32x8(xu + q * H + blk * 128, v, kHadNorm * WhtLaneSign());
+  }
+}
+
+// Routing, grouping and the input transforms of a decode call in one launch.  Workgroup 0
+// routes every row (16 waves, rows r, r + 16, ...), writes sel and wts, keeps the
+// selections in LDS and groups from there; every other workgroup routes its own row with
+// its first wave (the same deterministic result, kept in LDS only) and writes that row's
+// gate/up input transforms in route order, as GroupInputKernel does.
+template <int V>
+__global__ void __launch_bounds__(1024) RouteGroupInputKernel(const float* __restrict__ logits, int ld,
+                                                              const float* __restrict__ shared_logit,
+                                                              int* __restrict__ sel, float* __restrict__ wts,
+                                                              const void* __restrict__ x, int xf32, long long ldx,
+                                                              ExpertTables tb, int H, __half* __restrict__ xg,
+                                                              __half* __restrict__ xu, GroupOut o) {
+  __shared__ int s_sel[kSmallRoutes];
+  __shared__ int s_cur[kMaxExperts];
+  __shared__ int s_scan[128];
+  const int topk = o.topk, M = o.M, E = o.E;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (blockIdx.x == 0) {
+    for (int r = wave; r < M; r += 16) {
+      const float* lg = logits + (size_t)r * ld;
+      RouteRowWave<V>(lg, E, topk, shared_logit ? shared_logit[r] : lg[E], sel + (size_t)r * topk,
+                      wts + (size_t)r * (topk + 1), s_sel + r * topk);
+    }
+    __syncthreads();
+    GroupSmallBody(s_sel, o, s_cur, s_scan);
+    return;
+  }
+  const int nb = H / 128, j = threadIdx.x & 15;
+  const int items = (topk + 1) * nb, per = blockDim.x >> 4;
+  const int wpr = (items + per - 1) / per;
+  const int row = (blockIdx.x - 1) / wpr, part = (blockIdx.x - 1) % wpr;
+  int* s_e = s_sel;
+  if (wave == 0) {
+    const float* lg = logits + (size_t)row * ld;
+    RouteRowWave<V>(lg, E, topk, shared_logit ? shared_logit[row] : lg[E], nullptr, nullptr, s_e);
+    if (lane == 0) s_e[topk] = E;
+  }
+  (void)lane;
   __syncthreads();
   const size_t xr = (size_t)row * ldx;
   for (int it = part * per + (threadIdx.x >> 4); it < min(items, (part + 1) * per); it += per) {
@@ -988,9 +1045,31 @@ int MoeForward(const cx_moe_plan* pl, const void* x, int32_t x_dtype, int32_t ld
   mark();
   GroupOut o{counts, offsets, pairs, rows, inv, rexp, ent, nent, sz.chunk, M, pl->topk, pl->E, sz.max_entries};
   const bool front = !sz.prefill && FrontEndFits(M, pl->E, pl->topk);
-  LaunchRoute(logits, ld, M, pl->E, pl->topk, shared_logit, sel, wts, s);
-  mark();
-  if (front) {
+  // Routing fused into the grouping launch when workgroup 0 routes every row in one round
+  // of its 16 waves (M <= 16; CX_FUSED_ROUTE = 0 / 1 forces it off / on for any small call).
+  static const int fused_route_env = [] {
+    const char* e = std::getenv("CX_FUSED_ROUTE");
+    return e ? std::atoi(e) : -1;
+  }();
+  const bool fused_route = fused_route_env < 0 ? M <= 16 : fused_route_env != 0;
+  if (front && fused_route) {
+    // Routing, grouping and input transforms in one launch; the trace records it as the
+    // route stage (group and input stages empty).
+    const int wpr = ((pl->topk + 1) * (pl->H / 128) + 63) / 64;
+    if (pl->E <= 512)
+      hipLaunchKernelGGL(RouteGroupInputKernel<8>, dim3(1 + M * wpr), dim3(1024), 0, s, logits, ld, shared_logit, sel,
+                         wts, x, (int)(x_dtype == CX_F32), (long long)ldx, pl->tb, pl->H, xg, xu, o);
+    else
+      hipLaunchKernelGGL(RouteGroupInputKernel<16>, dim3(1 + M * wpr), dim3(1024), 0, s, logits, ld, shared_logit, sel,
+                         wts, x, (int)(x_dtype == CX_F32), (long long)ldx, pl->tb, pl->H, xg, xu, o);
+    mark();
+    mark();
+  } else {
+    LaunchRoute(logits, ld, M, pl->E, pl->topk, shared_logit, sel, wts, s);
+    mark();
+  }
+  if (front && fused_route) {
+  } else if (front) {
     // Grouping and input transforms in one launch; the trace records it as the group
     // stage (input stage empty).
     const int wpr = ((pl->topk + 1) * (pl->H / 128) + 63) / 64;
