@@ -725,9 +725,10 @@ namespace cx {
 // entry of up to 64 NRBW rows, and every activation fragment is loaded by exactly one
 // wave, straight into registers (no activation staging, no sharing needed).
 //
-// Step pipeline (one workgroup barrier per step, B fragments double buffered):
-//   barrier s | read B(s) from LDS | MFMAs of step s, decode of step s + 1 | write B(s + 1)
-// The buffer written for step s + 1 was last read for step s - 1, before barrier s.
+// Step pipeline (B fragments in 4 LDS buffers, decode two steps ahead of the MFMAs):
+//   [barrier at even s] | read B(s) | MFMAs of step s, decode of step s + 2 | write B(s + 2)
+// One workgroup barrier per two steps: every B write and its reads, and every read and the
+// next write of its buffer, have an even step's barrier between them.
 template <int K2, int CB, int NRBW>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 Exl3GemmTallKernel(GemmArgs g) {
@@ -736,7 +737,7 @@ Exl3GemmTallKernel(GemmArgs g) {
   constexpr int DPL = (SD + 63) / 64;
   constexpr int ND = WindowDwords(K2);
   constexpr int ER = 16;                       // epilogue slab rows (one row block)
-  constexpr int BBYTES = 2 * 4 * 2 * 64 * 16;  // [buffer][column pair][fragment][lane] x 16 B
+  constexpr int BBYTES = 4 * 4 * 2 * 64 * 16;  // [buffer][column pair][fragment][lane] x 16 B
   constexpr int EBYTES = 4 * ER * 132 * 4;     // one slab per wave
   __shared__ uint32_t stage[4][StageDwords<K2, DPL>()];
   __shared__ __align__(16) char smem[BBYTES > EBYTES ? BBYTES : EBYTES];
@@ -813,36 +814,42 @@ Exl3GemmTallKernel(GemmArgs g) {
     for (int k = 0; k < PFA; ++k)
 #pragma unroll
       for (int i = 0; i < NA; ++i) aq[k][i] = BufLoad128(rx, xoff[i], (uint32_t)k * 64);
-    {  // step 0 decoded and published, step 1 staged
-      stage_w(wq[0]);
-      wq[0] = BufLoadN<DPL>(rw, loff, (uint32_t)PFW * SD * 4);
+    // Steps 0 and 1 decoded and published, step 2 staged.
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      stage_w(wq[k]);
+      wq[k] = BufLoadN<DPL>(rw, loff, (uint32_t)(PFW + k) * SD * 4);
       __builtin_amdgcn_wave_barrier();
       uint32_t v[2][3];
       read_windows(v);
       __builtin_amdgcn_wave_barrier();
       half8_t b0, b1;
       decode(v, b0, b1);
-      write_b(0, b0, b1);
-      stage_w(wq[1]);
-      wq[1] = BufLoadN<DPL>(rw, loff, (uint32_t)(PFW + 1) * SD * 4);
+      write_b(k, b0, b1);
     }
-    constexpr int UN = 4;  // lcm(PFW, PFA, 2): fixed queue slots and buffers per unrolled step
+    stage_w(wq[0]);
+    wq[0] = BufLoadN<DPL>(rw, loff, (uint32_t)(PFW + 2) * SD * 4);
+    // Decode runs two steps ahead of the MFMAs into 4 B buffers (buffer s % 4), so a
+    // workgroup barrier is needed at even steps only: B(s + 2), written in step s, is read
+    // in step s + 2 with the even step's barrier in between, and buffer (s + 2) % 4 was last
+    // read in step s - 2, also one barrier earlier.
+    constexpr int UN = 4;  // lcm(PFW, PFA, 4 buffers): fixed queue slots and buffers per unrolled step
     constexpr int NM = NA * 8;  // MFMAs per step
     for (int s0 = 0; s0 < steps; s0 += UN) {
 #pragma unroll
       for (int u = 0; u < UN; ++u) {
         const int s = s0 + u;
-        __syncthreads();
+        if ((u & 1) == 0) __syncthreads();
         half8_t bf[4][2];
 #pragma unroll
         for (int c = 0; c < 4; ++c)
 #pragma unroll
-          for (int f = 0; f < 2; ++f) bf[c][f] = __builtin_bit_cast(half8_t, bs[(((u & 1) * 4 + c) * 2 + f) * 64 + lane]);
+          for (int f = 0; f < 2; ++f) bf[c][f] = __builtin_bit_cast(half8_t, bs[((u * 4 + c) * 2 + f) * 64 + lane]);
         uint32_t v[2][3];
-        read_windows(v);  // step s + 1, staged in the previous step
+        read_windows(v);  // step s + 2, staged in the previous step
         __builtin_amdgcn_sched_barrier(0);
         // MFMAs of step s (column-tile major, so the first ones need only the first B
-        // fragment) interleaved with the decode of step s + 1: the matrix core and the
+        // fragment) interleaved with the decode of step s + 2: the matrix core and the
         // VALU work side by side within the wave.
         half8_t n0, n1;
         decode(v, n0, n1);
@@ -865,9 +872,9 @@ Exl3GemmTallKernel(GemmArgs g) {
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         }
         __builtin_amdgcn_sched_barrier(0);
-        write_b((u + 1) & 1, n0, n1);  // step s + 1 (past the last step: never read)
-        stage_w(wq[u % PFW]);          // step s + 2
-        wq[u % PFW] = BufLoadN<DPL>(rw, loff, (uint32_t)(s + 2 + PFW) * SD * 4);
+        write_b((u + 2) & 3, n0, n1);  // step s + 2 (past the last step: never read)
+        stage_w(wq[(u + 1) % PFW]);    // step s + 3
+        wq[(u + 1) % PFW] = BufLoadN<DPL>(rw, loff, (uint32_t)(s + 3 + PFW) * SD * 4);
       }
     }
     __syncthreads();  // every wave is done with the B buffers: the epilogue reuses them
