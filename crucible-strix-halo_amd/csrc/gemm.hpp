@@ -737,7 +737,11 @@ Exl3GemmTallKernel(GemmArgs g) {
   constexpr int DPL = (SD + 63) / 64;
   constexpr int ND = WindowDwords(K2);
   constexpr int ER = 16;                       // epilogue slab rows (one row block)
-  constexpr int BBYTES = 4 * 4 * 2 * 64 * 16;  // [buffer][column pair][fragment][lane] x 16 B
+  // Steps the decode runs ahead of the MFMAs (one workgroup barrier per DA steps).
+  // Measured on config 5: 1 and 4 no better than 2 (4: gate/up -1.5%, down +1%).
+  constexpr int DA = 2;
+  constexpr int NBB = 2 * DA;        // B buffers
+  constexpr int BBYTES = NBB * 4 * 2 * 64 * 16;  // [buffer][column pair][fragment][lane] x 16 B
   constexpr int EBYTES = 4 * ER * 132 * 4;     // one slab per wave
   __shared__ uint32_t stage[4][StageDwords<K2, DPL>()];
   __shared__ __align__(16) char smem[BBYTES > EBYTES ? BBYTES : EBYTES];
@@ -814,11 +818,11 @@ Exl3GemmTallKernel(GemmArgs g) {
     for (int k = 0; k < PFA; ++k)
 #pragma unroll
       for (int i = 0; i < NA; ++i) aq[k][i] = BufLoad128(rx, xoff[i], (uint32_t)k * 64);
-    // Steps 0 and 1 decoded and published, step 2 staged.
+    // Steps 0 .. DA - 1 decoded and published, step DA staged.
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      stage_w(wq[k]);
-      wq[k] = BufLoadN<DPL>(rw, loff, (uint32_t)(PFW + k) * SD * 4);
+    for (int k = 0; k < DA; ++k) {
+      stage_w(wq[k % PFW]);
+      wq[k % PFW] = BufLoadN<DPL>(rw, loff, (uint32_t)(PFW + k) * SD * 4);
       __builtin_amdgcn_wave_barrier();
       uint32_t v[2][3];
       read_windows(v);
@@ -827,26 +831,26 @@ Exl3GemmTallKernel(GemmArgs g) {
       decode(v, b0, b1);
       write_b(k, b0, b1);
     }
-    stage_w(wq[0]);
-    wq[0] = BufLoadN<DPL>(rw, loff, (uint32_t)(PFW + 2) * SD * 4);
+    stage_w(wq[DA % PFW]);
+    wq[DA % PFW] = BufLoadN<DPL>(rw, loff, (uint32_t)(PFW + DA) * SD * 4);
     // Decode runs two steps ahead of the MFMAs into 4 B buffers (buffer s % 4), so a
     // workgroup barrier is needed at even steps only: B(s + 2), written in step s, is read
     // in step s + 2 with the even step's barrier in between, and buffer (s + 2) % 4 was last
     // read in step s - 2, also one barrier earlier.
-    constexpr int UN = 4;  // lcm(PFW, PFA, 4 buffers): fixed queue slots and buffers per unrolled step
+    constexpr int UN = NBB > 4 ? NBB : 4;  // lcm(PFW, PFA, NBB): fixed queue slots and buffers per unrolled step
     constexpr int NM = NA * 8;  // MFMAs per step
     for (int s0 = 0; s0 < steps; s0 += UN) {
 #pragma unroll
       for (int u = 0; u < UN; ++u) {
         const int s = s0 + u;
-        if ((u & 1) == 0) __syncthreads();
+        if (u % DA == 0) __syncthreads();
         half8_t bf[4][2];
 #pragma unroll
         for (int c = 0; c < 4; ++c)
 #pragma unroll
-          for (int f = 0; f < 2; ++f) bf[c][f] = __builtin_bit_cast(half8_t, bs[((u * 4 + c) * 2 + f) * 64 + lane]);
+          for (int f = 0; f < 2; ++f) bf[c][f] = __builtin_bit_cast(half8_t, bs[(((u % NBB) * 4 + c) * 2 + f) * 64 + lane]);
         uint32_t v[2][3];
-        read_windows(v);  // step s + 2, staged in the previous step
+        read_windows(v);  // step s + DA, staged in the previous step
         __builtin_amdgcn_sched_barrier(0);
         // MFMAs of step s (column-tile major, so the first ones need only the first B
         // fragment) interleaved with the decode of step s + 2: the matrix core and the
@@ -872,9 +876,9 @@ Exl3GemmTallKernel(GemmArgs g) {
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         }
         __builtin_amdgcn_sched_barrier(0);
-        write_b((u + 2) & 3, n0, n1);  // step s + 2 (past the last step: never read)
-        stage_w(wq[(u + 1) % PFW]);    // step s + 3
-        wq[(u + 1) % PFW] = BufLoadN<DPL>(rw, loff, (uint32_t)(s + 3 + PFW) * SD * 4);
+        write_b((u + DA) % NBB, n0, n1);  // step s + DA (past the last step: never read)
+        stage_w(wq[(u + DA + 1) % PFW]);  // step s + DA + 1
+        wq[(u + DA + 1) % PFW] = BufLoadN<DPL>(rw, loff, (uint32_t)(s + DA + 1 + PFW) * SD * 4);
       }
     }
     __syncthreads();  // every wave is done with the B buffers: the epilogue reuses them
