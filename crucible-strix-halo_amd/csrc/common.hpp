@@ -183,9 +183,17 @@ __host__ __device__ constexpr int PermRow32(int p) {
 // of the quad's 32 is [pair k of lane 0, of lane 1, of lane 2, of lane 3].  A 4 x 4
 // transpose of the packed pairs across the quad (two DPP exchange rounds) gives every
 // lane one whole chunk, stored with one 16-byte write.  d: the block's first half.
+// The quad transpose of StorePerm32x8: on return h[q] is pair t of lane q, i.e. chunk t
+// (8 halves) of the quad's 32 in MFMA row order, for lane t = (lane & 15) & 3.
+__device__ __forceinline__ void Perm32x8Chunk(const float v[8], float scale, int (&h)[4]);
 __device__ __forceinline__ void StorePerm32x8(__half* d, const float v[8], float scale) {
   const int j = threadIdx.x & 15, t = j & 3;
   int h[4];
+  Perm32x8Chunk(v, scale, h);
+  *reinterpret_cast<int4*>(d + 32 * (j >> 2) + 8 * t) = make_int4(h[0], h[1], h[2], h[3]);
+}
+__device__ __forceinline__ void Perm32x8Chunk(const float v[8], float scale, int (&h)[4]) {
+  const int t = threadIdx.x & 3;
 #pragma unroll
   for (int k = 0; k < 4; ++k)
     h[k] = __builtin_bit_cast(int, __floats2half2_rn(v[2 * k] * scale, v[2 * k + 1] * scale));
@@ -216,7 +224,6 @@ __device__ __forceinline__ void StorePerm32x8(__half* d, const float v[8], float
     }
   }
   // Now h[q] is pair t of lane q: chunk t of the quad.
-  *reinterpret_cast<int4*>(d + 32 * (j >> 2) + 8 * t) = make_int4(h[0], h[1], h[2], h[3]);
 }
 __device__ __forceinline__ void H8ToF(const uint4& u, float v[8]) {
   const __half2* h = reinterpret_cast<const __half2*>(&u);
@@ -276,6 +283,35 @@ __device__ __forceinline__ u32x2_t BufLoad64(__amdgpu_buffer_rsrc_t r, uint32_t 
 __device__ __forceinline__ u32x4_t BufLoad128(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
 }
+// The same store through a buffer resource: the block at byte offset voff + soff (voff may
+// differ per lane group, soff is uniform), the lane's chunk at + (32 (j >> 2) + 8 t) * 2.
+__device__ __forceinline__ void StorePerm32x8Buf(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
+                                                 const float v[8], float scale) {
+  const int j = threadIdx.x & 15, t = j & 3;
+  int h[4];
+  Perm32x8Chunk(v, scale, h);
+  __builtin_amdgcn_raw_buffer_store_b128(u32x4_t{(uint32_t)h[0], (uint32_t)h[1], (uint32_t)h[2], (uint32_t)h[3]}, r,
+                                         voff + (uint32_t)(32 * (j >> 2) + 8 * t) * 2, soff, 0);
+}
+// StorePerm32x8Buf with the quad transpose through LDS instead of DPP exchanges: lane
+// (q, s) = (lane / 4, lane % 4) writes its pair k to dword 16 q + 4 (k ^ f(q)) + s of the
+// wave's 256-dword area (f(q) = (q >> 1) & 3: each of the four writes covers all 32 banks
+// per half wave), then reads its chunk t = s, 16 bytes at 16 q + 4 (t ^ f(q)) (8
+// consecutive lanes cover all banks).  A wave's LDS operations run in order, so no
+// barrier is needed; the area must be the calling wave's own.
+__device__ __forceinline__ void StorePerm32x8LdsBuf(uint32_t* area, __amdgpu_buffer_rsrc_t r, uint32_t voff,
+                                                    uint32_t soff, const float v[8], float scale) {
+  const int lane = threadIdx.x & 63, j = lane & 15, q = lane >> 2, t = lane & 3, f = (q >> 1) & 3;
+  uint32_t h[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    h[k] = __builtin_bit_cast(uint32_t, __floats2half2_rn(v[2 * k] * scale, v[2 * k + 1] * scale));
+#pragma unroll
+  for (int k = 0; k < 4; ++k) area[16 * q + 4 * (k ^ f) + t] = h[k];
+  const u32x4_t c = *reinterpret_cast<const u32x4_t*>(area + 16 * q + 4 * (t ^ f));
+  __builtin_amdgcn_raw_buffer_store_b128(c, r, voff + (uint32_t)(32 * (j >> 2) + 8 * t) * 2, soff, 0);
+}
+
 // N consecutive dwords (N = 1..4) from a buffer.
 template <int N>
 struct Dwords {

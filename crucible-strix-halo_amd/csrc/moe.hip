@@ -482,11 +482,13 @@ __global__ void __launch_bounds__(1024) GroupScatterKernel(const int* __restrict
 // long calls; short calls split rows for parallelism).  Compact-row order keeps the
 // writes sequential; walking routes in row order instead (reads shared, writes scattered
 // in 4 KB pieces) measured 8% slower.  engine/layers/moe_rows.h:102-125.
-__global__ void __launch_bounds__(256) MoeInputKernel(const void* __restrict__ x, int xf32, long long ldx,
+template <bool XF32>
+__global__ void __launch_bounds__(256) MoeInputKernel(const void* __restrict__ x, long long ldx,
                                                       const int* __restrict__ rexp,
                                                       const int* __restrict__ rows, ExpertTables tb, int M, int topk,
                                                       int E, int H, int S, __half* __restrict__ xg,
                                                       __half* __restrict__ xu) {
+  __shared__ __align__(16) uint32_t tarea[4][256];  // per-wave transpose areas
   const int P = M * topk + M;
   const int w = blockIdx.x * 4 + (int)(threadIdx.x >> 6);
   const int p = w / S, part = w % S;
@@ -502,31 +504,50 @@ __global__ void __launch_bounds__(256) MoeInputKernel(const void* __restrict__ x
   const __half* sg = tb.gate_suh + (size_t)e * H;
   const __half* su = tb.up_suh + (size_t)e * H;
   const int g = (threadIdx.x >> 4) & 3, j = threadIdx.x & 15;
-  const size_t xr = (size_t)row * ldx;
   const int nb = H / 128, st = 4 * S;
+  // Every row touched here is addressed through a buffer resource on its (wave-uniform)
+  // start: the lanes' offsets are 32-bit and each block's offset is the uniform soffset,
+  // no 64-bit address arithmetic per load and store.
+  constexpr int esz = XF32 ? 4 : 2;
+  const __amdgpu_buffer_rsrc_t rxr =
+      MakeRsrc(static_cast<const char*>(x) + (size_t)row * ldx * esz, (uint32_t)(H * esz));
+  const __amdgpu_buffer_rsrc_t rsg = MakeRsrc(sg, (uint32_t)H * 2), rsu = MakeRsrc(su, (uint32_t)H * 2);
+  const __amdgpu_buffer_rsrc_t rdg = MakeRsrc(xg + (size_t)p * H, (uint32_t)H * 2);
+  const __amdgpu_buffer_rsrc_t rdu = MakeRsrc(xu + (size_t)p * H, (uint32_t)H * 2);
   // Up to 4 blocks per lane group at a time: all their loads are issued before the first
   // transform, so a wave keeps 12 16-byte loads in flight instead of 3.
   for (int b0 = 4 * part + g; b0 < nb; b0 += 4 * st) {
+    const uint32_t e0 = (uint32_t)(b0 * 128 + 8 * j);  // the lane's first element, block b0
     uint4 rx[4], rg[4], ru[4];
-#pragma unroll
-    for (int it = 0; it < 4; ++it)
-      if (b0 + it * st < nb) rx[it] = LoadAsH8(x, xf32, xr + (b0 + it * st) * 128 + 8 * j);
+    // Loads are unconditional: past the row's end they fall outside the buffer resource (no
+    // memory access, zeros) and are not used.
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
-      const int c0 = (b0 + it * st) * 128 + 8 * j;
-      if (b0 + it * st < nb) {
-        rg[it] = *reinterpret_cast<const uint4*>(sg + c0);
-        ru[it] = *reinterpret_cast<const uint4*>(su + c0);
+        const uint32_t so = (uint32_t)(it * st * 128);  // block it's element offset (uniform)
+        if constexpr (XF32) {
+          const u32x4_t lo = BufLoad128(rxr, e0 * 4, so * 4), hi = BufLoad128(rxr, e0 * 4 + 16, so * 4);
+          rx[it] = make_uint4(__builtin_bit_cast(uint32_t, __floats2half2_rn(__uint_as_float(lo[0]), __uint_as_float(lo[1]))),
+                              __builtin_bit_cast(uint32_t, __floats2half2_rn(__uint_as_float(lo[2]), __uint_as_float(lo[3]))),
+                              __builtin_bit_cast(uint32_t, __floats2half2_rn(__uint_as_float(hi[0]), __uint_as_float(hi[1]))),
+                              __builtin_bit_cast(uint32_t, __floats2half2_rn(__uint_as_float(hi[2]), __uint_as_float(hi[3]))));
+        } else {
+          const u32x4_t u = BufLoad128(rxr, e0 * 2, so * 2);
+          rx[it] = make_uint4(u[0], u[1], u[2], u[3]);
+        }
+        const u32x4_t a = BufLoad128(rsg, e0 * 2, so * 2), b = BufLoad128(rsu, e0 * 2, so * 2);
+        rg[it] = make_uint4(a[0], a[1], a[2], a[3]);
+        ru[it] = make_uint4(b[0], b[1], b[2], b[3]);
       }
-    }
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
       const int blk = b0 + it * st;
       if (blk >= nb) break;  // uniform over the 16-lane group
       float a[8], v[8];
       InputPairTransform(rx[it], rg[it], ru[it], a, v);
-      StorePerm32x8(xg + (size_t)p * H + blk * 128, a, kHadNorm * WhtLaneSign());
-      StorePerm32x8(xu + (size_t)p * H + blk * 128, v, kHadNorm * WhtLaneSign());
+      const uint32_t so = (uint32_t)(it * st * 128) * 2;
+      uint32_t* ta = tarea[threadIdx.x >> 6];
+      StorePerm32x8LdsBuf(ta, rdg, (uint32_t)(b0 * 128) * 2, so, a, kHadNorm * WhtLaneSign());
+      StorePerm32x8LdsBuf(ta, rdu, (uint32_t)(b0 * 128) * 2, so, v, kHadNorm * WhtLaneSign());
     }
   }
 }
@@ -1081,9 +1102,13 @@ int MoeForward(const cx_moe_plan* pl, const void* x, int32_t x_dtype, int32_t ld
     mark();
     // Split rows over more waves when there are few of them (decode).
     const int S = sz.P >= 4096 ? 1 : std::max(1, std::min(4, pl->H / 512));
-    hipLaunchKernelGGL(MoeInputKernel, dim3((unsigned)(((long)sz.P * S + 3) / 4)), dim3(256), 0, s,
-                       x, (int)(x_dtype == CX_F32), (long long)ldx, rexp, rows, pl->tb, M, pl->topk, pl->E, pl->H, S,
-                       xg, xu);
+    const dim3 grid((unsigned)(((long)sz.P * S + 3) / 4));
+    if (x_dtype == CX_F32)
+      hipLaunchKernelGGL(MoeInputKernel<true>, grid, dim3(256), 0, s, x, (long long)ldx, rexp, rows, pl->tb, M, pl->topk,
+                         pl->E, pl->H, S, xg, xu);
+    else
+      hipLaunchKernelGGL(MoeInputKernel<false>, grid, dim3(256), 0, s, x, (long long)ldx, rexp, rows, pl->tb, M,
+                         pl->topk, pl->E, pl->H, S, xg, xu);
   }
   mark();
   if (!LaunchExpertGemm(pl, sz, true, xg, xu, yg, yu, nullptr, xd, ent, nent, front ? pairs : nullptr, s))
