@@ -600,27 +600,43 @@ template <bool HC, bool F16>
 __global__ void __launch_bounds__(256) MoeCombineKernel(const void* __restrict__ pd, const float* __restrict__ psc,
                                                         const float* __restrict__ wts, const int* __restrict__ inv,
                                                         int M, int topk, int H, float* __restrict__ y, HcArgs hc) {
-  const int nq = H / 4;
+  // Columns per thread: 8 for fp16 rows (one 16-byte load per slot), 4 for fp32 rows.
+  constexpr int CW = F16 ? 8 : 4;
+  const int nq = H / CW;
   const int item = blockIdx.x * blockDim.x + threadIdx.x;
   if (item >= M * nq) return;
-  const int r = item / nq, c0 = (item % nq) * 4;
+  const int r = item / nq, c0 = (item % nq) * CW;
   auto slot_row = [&](int k) { return k < topk ? inv[r * topk + k] : M * topk + r; };
-  auto load = [&](int p) {
-    if constexpr (F16) {
-      const uint2 u = *reinterpret_cast<const uint2*>(static_cast<const __half*>(pd) + (size_t)p * H + c0);
-      const float sc = psc[(size_t)p * (H / 128) + c0 / 128];
-      const float2 a = __half22float2(__builtin_bit_cast(__half2, u.x)), b = __half22float2(__builtin_bit_cast(__half2, u.y));
-      return make_float4(a.x * sc, a.y * sc, b.x * sc, b.y * sc);
-    } else {
-      return *reinterpret_cast<const float4*>(static_cast<const float*>(pd) + (size_t)p * H + c0);
-    }
+  struct Cols {
+    float v[CW];
   };
-  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  auto add = [&](float w, float4 d) {
-    acc.x = CombineStep(acc.x, w, d.x);
-    acc.y = CombineStep(acc.y, w, d.y);
-    acc.z = CombineStep(acc.z, w, d.z);
-    acc.w = CombineStep(acc.w, w, d.w);
+  auto load = [&](int p) {
+    Cols d;
+    if constexpr (F16) {
+      const uint4 u = *reinterpret_cast<const uint4*>(static_cast<const __half*>(pd) + (size_t)p * H + c0);
+      const float sc = psc[(size_t)p * (H / 128) + c0 / 128];
+      const uint32_t h[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float2 f = __half22float2(__builtin_bit_cast(__half2, h[k]));
+        d.v[2 * k] = f.x * sc;
+        d.v[2 * k + 1] = f.y * sc;
+      }
+    } else {
+      const float4 f = *reinterpret_cast<const float4*>(static_cast<const float*>(pd) + (size_t)p * H + c0);
+      d.v[0] = f.x;
+      d.v[1] = f.y;
+      d.v[2] = f.z;
+      d.v[3] = f.w;
+    }
+    return d;
+  };
+  float acc[CW];
+#pragma unroll
+  for (int i = 0; i < CW; ++i) acc[i] = 0.f;
+  auto add = [&](float w, const Cols& d) {
+#pragma unroll
+    for (int i = 0; i < CW; ++i) acc[i] = CombineStep(acc[i], w, d.v[i]);
   };
   if (topk < kCombineSlots) {
     // All slot rows, then all their loads, issued before the first use (the rows and
@@ -628,7 +644,7 @@ __global__ void __launch_bounds__(256) MoeCombineKernel(const void* __restrict__
     // latency per stage instead of one per slot.
     int p[kCombineSlots];
     float w[kCombineSlots];
-    float4 d[kCombineSlots];
+    Cols d[kCombineSlots];
 #pragma unroll
     for (int k = 0; k < kCombineSlots; ++k) {
       p[k] = slot_row(min(k, topk));
@@ -642,19 +658,24 @@ __global__ void __launch_bounds__(256) MoeCombineKernel(const void* __restrict__
   } else {
     for (int k = 0; k <= topk; ++k) add(wts[(size_t)r * (topk + 1) + k], load(slot_row(k)));
   }
-  if constexpr (HC) {
-    for (int st = 0; st < hc.n_streams; ++st) {
-      const float g = hc.post[(size_t)r * hc.n_streams + st];
-      float4* h = reinterpret_cast<float4*>(hc.H + (size_t)r * hc.ldh + (size_t)st * H + c0);
-      float4 v = *h;
-      v.x = CombineStep(v.x, g, acc.x);
-      v.y = CombineStep(v.y, g, acc.y);
-      v.z = CombineStep(v.z, g, acc.z);
-      v.w = CombineStep(v.w, g, acc.w);
-      *h = v;
+#pragma unroll
+  for (int h4 = 0; h4 < CW / 4; ++h4) {
+    const float4 a = make_float4(acc[4 * h4], acc[4 * h4 + 1], acc[4 * h4 + 2], acc[4 * h4 + 3]);
+    const int c = c0 + 4 * h4;
+    if constexpr (HC) {
+      for (int st = 0; st < hc.n_streams; ++st) {
+        const float g = hc.post[(size_t)r * hc.n_streams + st];
+        float4* h = reinterpret_cast<float4*>(hc.H + (size_t)r * hc.ldh + (size_t)st * H + c);
+        float4 v = *h;
+        v.x = CombineStep(v.x, g, a.x);
+        v.y = CombineStep(v.y, g, a.y);
+        v.z = CombineStep(v.z, g, a.z);
+        v.w = CombineStep(v.w, g, a.w);
+        *h = v;
+      }
+    } else {
+      *reinterpret_cast<float4*>(y + (size_t)r * H + c) = a;
     }
-  } else {
-    *reinterpret_cast<float4*>(y + (size_t)r * H + c0) = acc;
   }
 }
 
@@ -1122,7 +1143,7 @@ int MoeForward(const cx_moe_plan* pl, const void* x, int32_t x_dtype, int32_t ld
     return CX_E_UNSUPPORTED;
   mark();
   {
-    const long items = (long)M * (pl->H / 4);
+    const long items = (long)M * (pl->H / (sz.prefill ? 8 : 4));  // columns per thread: MoeCombineKernel's CW
     const dim3 grid((unsigned)((items + 255) / 256));
     const HcArgs h = hc ? *hc : HcArgs{};
     if (hc && sz.prefill)
