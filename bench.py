@@ -367,7 +367,9 @@ def bench_r1(plans, seed, calls=200, warmup=50):
     lgs = [torch.randn(1, E + 1, generator=g, device="cuda") for _ in range(8)]
     ws = torch.empty(max(p.workspace_size(1, CX_MOE_DECODE) for p in plans), dtype=torch.uint8, device="cuda")
     y = torch.empty(1, H, dtype=torch.float32, device="cuda")
-    n_launch = 5  # route + grouping + input transforms (one launch at M <= 16), gate/up, mid, down, combine
+    # route + grouping + input transforms (one launch at M <= 16), gate/up, down (the mid in
+    # its prologue at small M unless CX_DOWN_MID=0 makes it a launch of its own), combine
+    n_launch = 5 if os.environ.get("CX_DOWN_MID") == "0" else 4
 
     def call(i):
         plans[i % len(plans)](xs[i % 8], lgs[i % 8], mode=CX_MOE_DECODE, workspace=ws, y=y)

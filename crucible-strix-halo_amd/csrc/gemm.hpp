@@ -125,14 +125,23 @@ struct GemmArgs {
   // (MFMA row order), row p at xd + p * O.
   const __half* mid_suh;
   __half* mid_xd;
+  // Decode down GEMM with the mid in its prologue (Exl3GemmKernel<..., MIDX = true>): the
+  // gate/up raw sums [rows][I] fp32 (compact row order) and the packed gate / up output
+  // scales [E + 1][I]; the down input scales are mid_suh.  The workgroup transforms its
+  // entry's rows into LDS and never reads plane.x.
+  const float* mid_yg;
+  const float* mid_yu;
+  const __half* mid_svg;
+  const __half* mid_svu;
 };
 
 // The mid of one row's 128-column block on 16 lanes (lane j: columns c0 + 8j..8j+7): the
 // gate and up output transforms of the raw sums gv, uv (fp32: WHT128 * norm * svh), then
 // RoundH(RoundH(SiLU(g) * u) * suh_down), WHT128, * norm -> fp16 in MFMA row order at dst
 // (the block's first half).  engine/layers/moe_rows.h:543-566.
-__device__ __forceinline__ void MidBlock(float gv[8], float uv[8], const __half* svg_p, const __half* svu_p,
-                                         const __half* sud_p, __half* dst) {
+// The values before the fp16 store (v times kHadNorm * WhtLaneSign() is the stored row).
+__device__ __forceinline__ void MidValues(float gv[8], float uv[8], const __half* svg_p, const __half* svu_p,
+                                          const __half* sud_p, float v[8]) {
   float svg[8], svu[8], sud[8];
   LoadH8(svg_p, svg);
   LoadH8(svu_p, svu);
@@ -145,7 +154,6 @@ __device__ __forceinline__ void MidBlock(float gv[8], float uv[8], const __half*
   Wht128x8Signed(gv);
   Wht128x8Signed(uv);
   const float sg = WhtLaneSign();
-  float v[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const float a = gv[i] * (sg * (kHadNorm * svg[i]));
@@ -153,7 +161,12 @@ __device__ __forceinline__ void MidBlock(float gv[8], float uv[8], const __half*
     v[i] = RoundH(RoundH(SiLU(a) * b) * sud[i]);
   }
   Wht128x8Signed(v);
-  StorePerm32x8(dst, v, kHadNorm * sg);
+}
+__device__ __forceinline__ void MidBlock(float gv[8], float uv[8], const __half* svg_p, const __half* svu_p,
+                                         const __half* sud_p, __half* dst) {
+  float v[8];
+  MidValues(gv, uv, svg_p, svu_p, sud_p, v);
+  StorePerm32x8(dst, v, kHadNorm * WhtLaneSign());
 }
 
 // Wave-uniform load through the scalar cache (device tables written by earlier launches).
@@ -185,10 +198,18 @@ __device__ __forceinline__ MatPtr MatOf(const GemmArgs& g, const GemmPlane& pl, 
 // (`x` at the first row, 32 k-columns per step starting at step 0) into acc.
 // `x` is the activation base at the wave's first k column; xrow[rb] is the byte offset of
 // the lane's row of block rb (at or beyond x_bytes: a row of zeros, no memory access).
-template <int K2, int CB, int NRB, int U>
+// XL: the activations come from LDS instead (xl at the lane's row and k-group, 16-byte
+// units, 4 per step); x, x_bytes and xrow are then unused, and fill() (which writes them,
+// all waves of the workgroup together) runs after the first weight loads are issued, so
+// their latency overlaps it.
+struct NoFill {
+  __device__ void operator()() const {}
+};
+template <int K2, int CB, int NRB, int U, bool XL = false, typename Fill = NoFill>
 __device__ __forceinline__ void StreamColumnPair(const uint32_t* tiles, int steps, const __half* x, uint32_t x_bytes,
                                                  const uint32_t (&xrow)[NRB], uint32_t* slot, int lane,
-                                                 float4_t (&acc)[NRB][2]) {
+                                                 float4_t (&acc)[NRB][2], const u32x4_t* xl = nullptr,
+                                                 Fill&& fill = Fill{}) {
   constexpr int T = TileDwords(K2);    // dwords per tile
   constexpr int SD = 4 * T;            // dwords per step
   constexpr int DPL = (SD + 63) / 64;  // dwords each lane loads per step
@@ -211,7 +232,12 @@ __device__ __forceinline__ void StreamColumnPair(const uint32_t* tiles, int step
   for (int rb = 0; rb < NRB; ++rb) acc[rb][0] = acc[rb][1] = float4_t{0.f, 0.f, 0.f, 0.f};
 
   auto load_w = [&](int s) { return BufLoadN<DPL>(rw, loff, (uint32_t)s * SD * 4); };
-  auto load_x = [&](int s, int rb) { return BufLoad128(rx, xoff[rb], (uint32_t)s * 64); };
+  auto load_x = [&](int s, int rb) {
+    if constexpr (XL)
+      return xl[s * 4];
+    else
+      return BufLoad128(rx, xoff[rb], (uint32_t)s * 64);
+  };
   auto step = [&](const Dwords<DPL>& w, const u32x4_t (&xv)[NRB]) {
     // Stage the step in the wave's slot; LDS executes a wave's operations in order, so
     // the window reads below see these writes and the next step's writes follow them.
@@ -254,7 +280,17 @@ __device__ __forceinline__ void StreamColumnPair(const uint32_t* tiles, int step
       for (int rb = 0; rb < NRB; ++rb) xg[u][rb] = load_x(sb + u, rb);
     }
   };
-  load_group(wa, xa, 0);
+  if constexpr (XL) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) wa[u] = load_w(u);
+    fill();
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int rb = 0; rb < NRB; ++rb) xa[u][rb] = load_x(u, rb);
+  } else {
+    load_group(wa, xa, 0);
+  }
   for (int s = 0; s < steps; s += 2 * U) {
     load_group(wb, xb, s + U);
 #pragma unroll
@@ -270,9 +306,18 @@ __device__ __forceinline__ void StreamColumnPair(const uint32_t* tiles, int step
 // One 16-row block per wave (decode) at up to 4 bpw asks for 8 waves per SIMD (64
 // registers, no spills there): the decode is VALU-bound and the extra waves hide the
 // LDS round trip of each step.
-template <int K2, int CB, int NRB, int KSW, int U>
+//
+// MIDX (one row block, no K split): the down projection of the decode MoE layer with the
+// mid computed in the prologue.  The workgroup transforms its entry's rows (at most 16)
+// from the gate/up sums into LDS in MFMA row order (dynamic LDS: 16 rows of I + 8 halves;
+// the pad keeps the 16 rows of a k-group in distinct banks), and the K loop reads them
+// there; rows past the entry read its last row (their sums are discarded).  Each of the
+// entry's column-block workgroups computes the mid again: a few hundred VALU per row
+// block instead of a launch and the down input's round trip through memory.
+template <int K2, int CB, int NRB, int KSW, int U, bool MIDX = false>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NRB == 1 && K2 <= 8 ? 8 : 1)))
 Exl3GemmKernel(GemmArgs g) {
+  static_assert(!MIDX || (NRB == 1 && KSW == 1), "the prologue mid is for the decode down projection");
   constexpr int CPW = 4 / KSW;
   constexpr int T = TileDwords(K2);
   constexpr int DPL = (4 * T + 63) / 64;
@@ -314,8 +359,35 @@ Exl3GemmKernel(GemmArgs g) {
     xbytes = (uint32_t)nrows * pl.ldx * 2;
   }
   float4_t acc[NRB][2];
-  StreamColumnPair<K2, CB, NRB, U>(m.tiles + ((size_t)cp * g.A + a0) * 2 * T, steps, xb, xbytes, xrow, stage[wave],
-                                   lane, acc);
+  extern __shared__ u32x4_t xmid[];  // MIDX only (no dynamic LDS otherwise)
+  if constexpr (MIDX) {
+    const int I = g.A * 16, nb = I / 128, rs = I / 8 + 1;  // 16-byte units per LDS row
+    auto fill = [&]() {
+      const int e = ent.x, j = lane & 15;
+      const __half* svg = g.mid_svg + (size_t)e * I;
+      const __half* svu = g.mid_svu + (size_t)e * I;
+      const __half* sud = g.mid_suh + (size_t)e * I;
+      for (int it = (int)threadIdx.x >> 4; it < nrows * nb; it += 16) {  // uniform per 16 lanes
+        const int r = it / nb, blk = it % nb, c0 = blk * 128 + 8 * j;
+        const size_t p = (size_t)(row0 + r);
+        float gv[8], uv[8], v[8];
+        LoadF8(g.mid_yg + p * I + c0, gv);
+        LoadF8(g.mid_yu + p * I + c0, uv);
+        MidValues(gv, uv, svg + c0, svu + c0, sud + c0, v);
+        int h[4];
+        Perm32x8Chunk(v, kHadNorm * WhtLaneSign(), h);
+        xmid[r * rs + blk * 16 + 4 * (j >> 2) + (j & 3)] =
+            u32x4_t{(uint32_t)h[0], (uint32_t)h[1], (uint32_t)h[2], (uint32_t)h[3]};
+      }
+      __syncthreads();
+    };
+    const int rr = min(lane & 15, nrows - 1);
+    StreamColumnPair<K2, CB, NRB, U, true>(m.tiles + ((size_t)cp * g.A + a0) * 2 * T, steps, xb, xbytes, xrow,
+                                           stage[wave], lane, acc, xmid + rr * rs + 2 * a0 + (lane >> 4), fill);
+  } else {
+    StreamColumnPair<K2, CB, NRB, U>(m.tiles + ((size_t)cp * g.A + a0) * 2 * T, steps, xb, xbytes, xrow, stage[wave],
+                                     lane, acc);
+  }
 
   if constexpr (KSW > 1) {
     // Fixed-order reduction of the K splits of each column pair.
@@ -342,8 +414,16 @@ Exl3GemmKernel(GemmArgs g) {
     if (pl.epi == 1) {
       // The workgroup holds columns [128 cpg, 128 cpg + 128): one whole output Hadamard
       // block.  Stage y_h in LDS, then WHT128 * norm * svh per row (engine LinOutBlock,
-      // engine/exl3/exl3.h:69-82), fp32.
-      __shared__ float ebuf[16 * NRB][132];
+      // engine/exl3/exl3.h:69-82), fp32.  MIDX: in the mid rows' LDS, once every wave is
+      // done with them (8.4 KB of the 16.6 KB; 8 workgroups per CU still fit).
+      float(*ebuf)[132];
+      if constexpr (MIDX) {
+        __syncthreads();
+        ebuf = reinterpret_cast<float(*)[132]>(xmid);
+      } else {
+        __shared__ float ebuf_s[16 * NRB][132];
+        ebuf = ebuf_s;
+      }
       const int cl = wave * 32 + ((lane & 15) >> 3) * 16 + (lane & 7);
 #pragma unroll
       for (int rb = 0; rb < NRB; ++rb)

@@ -15,6 +15,16 @@ bool CX_CAT(LaunchGemmRate, CX_RATE)(int cb, int nrb, int ksw, dim3 grid, const 
   constexpr int U = 2;  // step groups in flight per wave (fewer registers, more waves)
   auto go = [&](auto cbc, auto nrbc, auto kswc) {
     constexpr int CB = decltype(cbc)::value, NRB = decltype(nrbc)::value, KSW = decltype(kswc)::value;
+    if constexpr (NRB == 1 && KSW == 1) {
+      if (g.mid_yg) {  // the decode down projection with the mid in its prologue
+        // 16 rows of I + 8 halves, the up to 3 U - 1 steps (4 units each) the loop reads
+        // past the last one (results unused), and at least the epilogue's 16 x 132 floats
+        // it aliases
+        const size_t lds = std::max((size_t)(16 * (g.A * 2 + 1) + 12 * U) * 16, (size_t)16 * 132 * 4);
+        hipLaunchKernelGGL((Exl3GemmKernel<K2, CB, NRB, KSW, U, true>), grid, dim3(256), lds, s, g);
+        return true;
+      }
+    }
     hipLaunchKernelGGL((Exl3GemmKernel<K2, CB, NRB, KSW, U>), grid, dim3(256), 0, s, g);
     return true;
   };

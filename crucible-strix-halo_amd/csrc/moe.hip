@@ -699,7 +699,7 @@ namespace cx {
 
 struct MoeSizes {
   int M, P, n, nsh, chunk, nrb, wpg, max_entries, ntiles;
-  bool small, prefill, tall, mid;
+  bool small, prefill, tall, mid, down_mid;
   size_t off_sel, off_wts, off_counts, off_offsets, off_pairs, off_rows, off_inv, off_rexp, off_ent, off_nent, off_tiles;
   size_t off_xg, off_xu, off_yg, off_yu, off_xd, off_yd, off_ysc, total;
 };
@@ -745,6 +745,18 @@ MoeSizes PlanMoe(const cx_moe_plan* pl, int M, int mode) {
   // Register-blocked prefill: gate and up in one workgroup with the mid fused into the
   // epilogue (64-row entries, 4 waves per plane).
   s.mid = !decode && !s.tall && s.nrb == 4 && ps.mid;
+  // Decode: the mid in the down GEMM's prologue (16 rows of I halves in LDS per workgroup)
+  // while at most 128 entries can exist (M (topk + 1) <= 128): the down launch is then at
+  // most one generation of workgroups (16 per entry, 8 per CU), and the mid launch it
+  // saves is pure latency.  Measured on config 3: -2 to -2.5 us per layer at 1-8 rows, no
+  // change at 12-32, +2 to +4 us at 40 (every workgroup recomputes its entry's mid).
+  // Environment override: CX_DOWN_MID = 0 / 1 forces it off / on (decode, I <= 1024).
+  static const int down_mid_env = [] {
+    const char* e = std::getenv("CX_DOWN_MID");
+    return e ? std::atoi(e) : -1;
+  }();
+  s.down_mid = decode && pl->I <= 1024 &&
+               (down_mid_env < 0 ? (long)M * (pl->topk + 1) <= 128 : down_mid_env != 0);
   // Decode: one 16-row block per entry; prefill: every row of an entry shares each decoded tile.
   s.chunk = 16 * s.nrb;
   s.nsh = (M + s.chunk - 1) / s.chunk;
@@ -837,8 +849,14 @@ int LaunchGroup(const int* sel, GroupOut& o, int* tile_counts, int ntiles, hipSt
 // separate launches.
 bool LaunchExpertGemm(const cx_moe_plan* pl, const MoeSizes& sz, bool gate_up, const __half* xa, const __half* xb,
                       float* ya, float* yb, float* ysc, __half* xd, const int4* ent, const int* nent, const int* xmap,
-                      hipStream_t s) {
+                      const float* mid_yg, const float* mid_yu, hipStream_t s) {
   GemmArgs g{};
+  if (mid_yg) {
+    g.mid_yg = mid_yg;
+    g.mid_yu = mid_yu;
+    g.mid_svg = pl->tb.gate_svh;
+    g.mid_svu = pl->tb.up_svh;
+  }
   g.mid_suh = pl->tb.down_suh;
   g.mid_xd = xd;
   g.xmap = xmap;
@@ -1132,14 +1150,16 @@ int MoeForward(const cx_moe_plan* pl, const void* x, int32_t x_dtype, int32_t ld
                          pl->topk, pl->E, pl->H, S, xg, xu);
   }
   mark();
-  if (!LaunchExpertGemm(pl, sz, true, xg, xu, yg, yu, nullptr, xd, ent, nent, front ? pairs : nullptr, s))
+  if (!LaunchExpertGemm(pl, sz, true, xg, xu, yg, yu, nullptr, xd, ent, nent, front ? pairs : nullptr, nullptr, nullptr,
+                        s))
     return CX_E_UNSUPPORTED;
   mark();
-  if (!sz.mid)  // else the gate/up GEMM wrote the down projection's input rows itself
+  if (!sz.mid && !sz.down_mid)  // else a GEMM computes the down projection's input rows itself
     hipLaunchKernelGGL(MoeMidKernel, dim3((unsigned)((sz.P + 3) / 4)), dim3(256), 0, s, yg, yu, rexp,
                        pl->tb, M, pl->topk, pl->E, pl->I, xd);
   mark();
-  if (!LaunchExpertGemm(pl, sz, false, xd, nullptr, yd, nullptr, ysc, nullptr, ent, nent, nullptr, s))
+  if (!LaunchExpertGemm(pl, sz, false, xd, nullptr, yd, nullptr, ysc, nullptr, ent, nent, nullptr,
+                        sz.down_mid ? yg : nullptr, sz.down_mid ? yu : nullptr, s))
     return CX_E_UNSUPPORTED;
   mark();
   {
