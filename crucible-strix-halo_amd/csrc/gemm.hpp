@@ -133,6 +133,10 @@ struct GemmArgs {
   const float* mid_yu;
   const __half* mid_svg;
   const __half* mid_svu;
+  // Tall gate/up GEMM with the mid fused (grid z = 1): a workgroup runs plane 0 (gate),
+  // parks its raw sums in plane 0's y, runs plane 1 (up) and computes the mid of its rows
+  // into mid_xd from the parked gate sums and the up sums in registers.
+  int tall_seq_mid;
 };
 
 // The mid of one row's 128-column block on 16 lanes (lane j: columns c0 + 8j..8j+7): the
@@ -831,17 +835,15 @@ Exl3GemmTallKernel(GemmArgs g) {
   const int ei = gp.y + g.entry_base;
   if (ei >= n_entries) return;
   const int4 ent = EntryOf(g, ei);
-  const GemmPlane& pl = g.plane[gp.z];
+  const bool seq = g.tall_seq_mid != 0;  // both planes in this workgroup, the mid fused
   const int cpg = gp.x;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int steps = g.A / 2;
   const int row0 = ent.y, nrows = ent.z;
   if (nrows <= 0) return;
   const int nrb = (nrows + 15) / 16;
-  const MatPtr m = MatOf(g, pl, ent.x);
   const LaneRun<K2> lr(lane);
   const int cp = cpg * 4 + wave;
-  const __amdgpu_buffer_rsrc_t rw = MakeRsrc(m.tiles + (size_t)cp * g.A * 2 * T, (uint32_t)steps * SD * 4);
   uint32_t woff[2][ND];
 #pragma unroll
   for (int j = 0; j < 2; ++j)
@@ -849,8 +851,6 @@ Exl3GemmTallKernel(GemmArgs g) {
     for (int i = 0; i < ND; ++i) woff[j][i] = (uint32_t)StagePad<K2>((2 * j + lr.tile) * T + (lr.d0 + i) % T);
   const uint32_t loff = (uint32_t)lane * DPL * 4;
   uint32_t* slot = stage[wave];
-  // Activations: rows past the entry lie outside the buffer resource and read as zeros.
-  const __amdgpu_buffer_rsrc_t rx = MakeRsrc(pl.x + (size_t)row0 * pl.ldx, (uint32_t)nrows * pl.ldx * 2);
 
   // A step's weights go through the wave's LDS slot: staged (written) one step before its
   // decode, windows read back at the start of the decode's step.
@@ -879,98 +879,174 @@ Exl3GemmTallKernel(GemmArgs g) {
     constexpr int NA = decltype(nac)::value;  // row blocks per wave
     constexpr int PFW = 2;                    // weight steps in flight (beyond the staged one)
     constexpr int PFA = 2;                    // activation steps in flight
-    uint32_t xoff[NA];
+    for (int pz = seq ? 0 : gp.z;; ++pz) {  // one plane, or gate then up (seq)
+      const GemmPlane& pl = g.plane[pz];
+      const MatPtr m = MatOf(g, pl, ent.x);
+      const __amdgpu_buffer_rsrc_t rw = MakeRsrc(m.tiles + (size_t)cp * g.A * 2 * T, (uint32_t)steps * SD * 4);
+      // Activations: rows past the entry lie outside the buffer resource and read as zeros.
+      const __amdgpu_buffer_rsrc_t rx = MakeRsrc(pl.x + (size_t)row0 * pl.ldx, (uint32_t)nrows * pl.ldx * 2);
+      uint32_t xoff[NA];
 #pragma unroll
-    for (int i = 0; i < NA; ++i)
-      xoff[i] = (uint32_t)(((wave + 4 * i) * 16 + (lane & 15)) * pl.ldx * 2 + 16 * (lane >> 4));
-    float4_t acc[NA][4][2];
+      for (int i = 0; i < NA; ++i)
+        xoff[i] = (uint32_t)(((wave + 4 * i) * 16 + (lane & 15)) * pl.ldx * 2 + 16 * (lane >> 4));
+      float4_t acc[NA][4][2];
 #pragma unroll
-    for (int i = 0; i < NA; ++i)
+      for (int i = 0; i < NA; ++i)
 #pragma unroll
-      for (int c = 0; c < 4; ++c) acc[i][c][0] = acc[i][c][1] = float4_t{0.f, 0.f, 0.f, 0.f};
-    Dwords<DPL> wq[PFW];  // slot j % PFW: step j's weights until they are staged
-    u32x4_t aq[PFA][NA];
-    // Loads are unconditional, also past the last step (outside the buffer resources: no
-    // memory access, zeros), so the compiler can count the loads in flight.
+        for (int c = 0; c < 4; ++c) acc[i][c][0] = acc[i][c][1] = float4_t{0.f, 0.f, 0.f, 0.f};
+      Dwords<DPL> wq[PFW];  // slot j % PFW: step j's weights until they are staged
+      u32x4_t aq[PFA][NA];
+      // Loads are unconditional, also past the last step (outside the buffer resources: no
+      // memory access, zeros), so the compiler can count the loads in flight.
 #pragma unroll
-    for (int k = 0; k < PFW; ++k) wq[k] = BufLoadN<DPL>(rw, loff, (uint32_t)k * SD * 4);
+      for (int k = 0; k < PFW; ++k) wq[k] = BufLoadN<DPL>(rw, loff, (uint32_t)k * SD * 4);
 #pragma unroll
-    for (int k = 0; k < PFA; ++k)
+      for (int k = 0; k < PFA; ++k)
 #pragma unroll
-      for (int i = 0; i < NA; ++i) aq[k][i] = BufLoad128(rx, xoff[i], (uint32_t)k * 64);
-    // Steps 0 .. DA - 1 decoded and published, step DA staged.
+        for (int i = 0; i < NA; ++i) aq[k][i] = BufLoad128(rx, xoff[i], (uint32_t)k * 64);
+      // Steps 0 .. DA - 1 decoded and published, step DA staged.
 #pragma unroll
-    for (int k = 0; k < DA; ++k) {
-      stage_w(wq[k % PFW]);
-      wq[k % PFW] = BufLoadN<DPL>(rw, loff, (uint32_t)(PFW + k) * SD * 4);
-      __builtin_amdgcn_wave_barrier();
-      uint32_t v[2][3];
-      read_windows(v);
-      __builtin_amdgcn_wave_barrier();
-      half8_t b0, b1;
-      decode(v, b0, b1);
-      write_b(k, b0, b1);
-    }
-    stage_w(wq[DA % PFW]);
-    wq[DA % PFW] = BufLoadN<DPL>(rw, loff, (uint32_t)(PFW + DA) * SD * 4);
-    // Decode runs two steps ahead of the MFMAs into 4 B buffers (buffer s % 4), so a
-    // workgroup barrier is needed at even steps only: B(s + 2), written in step s, is read
-    // in step s + 2 with the even step's barrier in between, and buffer (s + 2) % 4 was last
-    // read in step s - 2, also one barrier earlier.
-    constexpr int UN = NBB > 4 ? NBB : 4;  // lcm(PFW, PFA, NBB): fixed queue slots and buffers per unrolled step
-    constexpr int NM = NA * 8;  // MFMAs per step
-    for (int s0 = 0; s0 < steps; s0 += UN) {
-#pragma unroll
-      for (int u = 0; u < UN; ++u) {
-        const int s = s0 + u;
-        if (u % DA == 0) __syncthreads();
-        half8_t bf[4][2];
-#pragma unroll
-        for (int c = 0; c < 4; ++c)
-#pragma unroll
-          for (int f = 0; f < 2; ++f) bf[c][f] = __builtin_bit_cast(half8_t, bs[(((u % NBB) * 4 + c) * 2 + f) * 64 + lane]);
+      for (int k = 0; k < DA; ++k) {
+        stage_w(wq[k % PFW]);
+        wq[k % PFW] = BufLoadN<DPL>(rw, loff, (uint32_t)(PFW + k) * SD * 4);
+        __builtin_amdgcn_wave_barrier();
         uint32_t v[2][3];
-        read_windows(v);  // step s + DA, staged in the previous step
-        __builtin_amdgcn_sched_barrier(0);
-        // MFMAs of step s (column-tile major, so the first ones need only the first B
-        // fragment) interleaved with the decode of step s + 2: the matrix core and the
-        // VALU work side by side within the wave.
-        half8_t n0, n1;
-        decode(v, n0, n1);
+        read_windows(v);
+        __builtin_amdgcn_wave_barrier();
+        half8_t b0, b1;
+        decode(v, b0, b1);
+        write_b(k, b0, b1);
+      }
+      stage_w(wq[DA % PFW]);
+      wq[DA % PFW] = BufLoadN<DPL>(rw, loff, (uint32_t)(PFW + DA) * SD * 4);
+      // Decode runs two steps ahead of the MFMAs into 4 B buffers (buffer s % 4), so a
+      // workgroup barrier is needed at even steps only: B(s + 2), written in step s, is read
+      // in step s + 2 with the even step's barrier in between, and buffer (s + 2) % 4 was last
+      // read in step s - 2, also one barrier earlier.
+      constexpr int UN = NBB > 4 ? NBB : 4;  // lcm(PFW, PFA, NBB): fixed queue slots and buffers per unrolled step
+      constexpr int NM = NA * 8;  // MFMAs per step
+      for (int s0 = 0; s0 < steps; s0 += UN) {
 #pragma unroll
-        for (int c = 0; c < 4; ++c)
+        for (int u = 0; u < UN; ++u) {
+          const int s = s0 + u;
+          if (u % DA == 0) __syncthreads();
+          half8_t bf[4][2];
 #pragma unroll
-          for (int f = 0; f < 2; ++f)
+          for (int c = 0; c < 4; ++c)
 #pragma unroll
-            for (int i = 0; i < NA; ++i)
-              acc[i][c][f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, aq[u % PFA][i]),
-                                                                    bf[c][f], acc[i][c][f], 0, 0, 0);
+            for (int f = 0; f < 2; ++f) bf[c][f] = __builtin_bit_cast(half8_t, bs[(((u % NBB) * 4 + c) * 2 + f) * 64 + lane]);
+          uint32_t v[2][3];
+          read_windows(v);  // step s + DA, staged in the previous step
+          __builtin_amdgcn_sched_barrier(0);
+          // MFMAs of step s (column-tile major, so the first ones need only the first B
+          // fragment) interleaved with the decode of step s + 2: the matrix core and the
+          // VALU work side by side within the wave.
+          half8_t n0, n1;
+          decode(v, n0, n1);
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int f = 0; f < 2; ++f)
+#pragma unroll
+              for (int i = 0; i < NA; ++i)
+                acc[i][c][f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, aq[u % PFA][i]),
+                                                                      bf[c][f], acc[i][c][f], 0, 0, 0);
+#pragma unroll
+          for (int i = 0; i < NA; ++i) {
+            aq[u % PFA][i] = BufLoad128(rx, xoff[i], (uint32_t)(s + PFA) * 64);
+          }
+          __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+#pragma unroll
+          for (int k = 0; k < NM - 2; ++k) {
+            __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+          write_b((u + DA) % NBB, n0, n1);  // step s + DA (past the last step: never read)
+          stage_w(wq[(u + DA + 1) % PFW]);  // step s + DA + 1
+          wq[(u + DA + 1) % PFW] = BufLoadN<DPL>(rw, loff, (uint32_t)(s + DA + 1 + PFW) * SD * 4);
+        }
+      }
+      __syncthreads();  // every wave is done with the B buffers: the epilogue reuses them
+
+      if (seq && pz == 1) {
+        // The mid of the wave's rows: up sums staged per row block in the wave's slab, gate
+        // sums read back from plane 0's y, where this wave wrote them (the workgroup
+        // barriers since then order the writes before these reads).
+        float(*eb)[132] = reinterpret_cast<float(*)[132]>(smem + wave * ER * 132 * 4);
+        const GemmPlane& p0 = g.plane[0];
+        const MatPtr mg = MatOf(g, p0, ent.x);
+        const int j = lane & 15, c0 = cpg * 128 + 8 * j, O = g.ncp * 32;
 #pragma unroll
         for (int i = 0; i < NA; ++i) {
-          aq[u % PFA][i] = BufLoad128(rx, xoff[i], (uint32_t)(s + PFA) * 64);
-        }
-        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+          const int rb = wave + 4 * i;
+          if (rb >= nrb) break;  // wave-uniform
 #pragma unroll
-        for (int k = 0; k < NM - 2; ++k) {
-          __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int cl = c * 32 + ((lane & 15) >> 3) * 16 + (lane & 7);
+              eb[4 * (lane >> 4) + e][cl] = acc[i][c][0][e];
+              eb[4 * (lane >> 4) + e][cl + 8] = acc[i][c][1][e];
+            }
+          __builtin_amdgcn_wave_barrier();
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int rr = 4 * q + (lane >> 4), r = rb * 16 + rr;
+            if (r < nrows) {  // uniform over the row's 16 lanes
+              const size_t p = (size_t)(row0 + r);
+              float gv[8], uv[8];
+              LoadF8(p0.y + p * p0.ldy + c0, gv);
+#pragma unroll
+              for (int e = 0; e < 8; ++e) uv[e] = eb[rr][8 * j + e];
+              MidBlock(gv, uv, mg.svh + c0, m.svh + c0, g.mid_suh + (size_t)ent.x * O + c0,
+                       g.mid_xd + p * O + cpg * 128);
+            }
+          }
+          __builtin_amdgcn_wave_barrier();
         }
-        __builtin_amdgcn_sched_barrier(0);
-        write_b((u + DA) % NBB, n0, n1);  // step s + DA (past the last step: never read)
-        stage_w(wq[(u + DA + 1) % PFW]);  // step s + DA + 1
-        wq[(u + DA + 1) % PFW] = BufLoadN<DPL>(rw, loff, (uint32_t)(s + DA + 1 + PFW) * SD * 4);
+        return;
       }
-    }
-    __syncthreads();  // every wave is done with the B buffers: the epilogue reuses them
-
-    if (pl.epi >= 1) {
-      // Output transform per row: the wave holds all 128 columns of its row blocks.
-      // Stage one row block (16 x 128 fp32) in the wave's slab, then WHT128 * norm * svh.
+      if (pl.epi >= 1) {
+        // Output transform per row: the wave holds all 128 columns of its row blocks.
+        // Stage one row block (16 x 128 fp32) in the wave's slab, then WHT128 * norm * svh.
+        float(*eb)[132] = reinterpret_cast<float(*)[132]>(smem + wave * ER * 132 * 4);
+        const int j = lane & 15;
+        const int c0 = cpg * 128 + 8 * j;
+        float sv[8];
+        LoadH8(m.svh + c0, sv);
+#pragma unroll
+        for (int i = 0; i < NA; ++i) {
+          const int rb = wave + 4 * i;
+          if (rb >= nrb) break;  // wave-uniform
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int cl = c * 32 + ((lane & 15) >> 3) * 16 + (lane & 7);
+              eb[4 * (lane >> 4) + e][cl] = acc[i][c][0][e];
+              eb[4 * (lane >> 4) + e][cl + 8] = acc[i][c][1][e];
+            }
+          __builtin_amdgcn_wave_barrier();
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int rr = 4 * q + (lane >> 4);
+            float v[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = 0.f + eb[rr][8 * j + e];
+            Wht128x8Signed(v);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] *= WhtLaneSign() * (kHadNorm * sv[e]);
+            const int r = rb * 16 + rr;
+            if (r < nrows) StoreBlockRow(pl, (size_t)(row0 + r), c0, g.ncp * 32, v);
+          }
+          __builtin_amdgcn_wave_barrier();
+        }
+        return;
+      }
+      // Raw sums: each row block (16 x 128 fp32) staged in the wave's slab and written as
+      // 16-byte pieces, 8 store instructions per lane instead of 32 single-float ones.
       float(*eb)[132] = reinterpret_cast<float(*)[132]>(smem + wave * ER * 132 * 4);
-      const int j = lane & 15;
-      const int c0 = cpg * 128 + 8 * j;
-      float sv[8];
-      LoadH8(m.svh + c0, sv);
 #pragma unroll
       for (int i = 0; i < NA; ++i) {
         const int rb = wave + 4 * i;
@@ -985,46 +1061,17 @@ Exl3GemmTallKernel(GemmArgs g) {
           }
         __builtin_amdgcn_wave_barrier();
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int rr = 4 * q + (lane >> 4);
-          float v[8];
-#pragma unroll
-          for (int e = 0; e < 8; ++e) v[e] = 0.f + eb[rr][8 * j + e];
-          Wht128x8Signed(v);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) v[e] *= WhtLaneSign() * (kHadNorm * sv[e]);
+        for (int k = 0; k < 8; ++k) {
+          const int rr = 2 * k + (lane >> 5), c4 = 4 * (lane & 31);
           const int r = rb * 16 + rr;
-          if (r < nrows) StoreBlockRow(pl, (size_t)(row0 + r), c0, g.ncp * 32, v);
+          if (r < nrows)
+            *reinterpret_cast<float4*>(pl.y + (size_t)(row0 + r) * pl.ldy + cpg * 128 + c4) =
+                *reinterpret_cast<const float4*>(&eb[rr][c4]);
         }
         __builtin_amdgcn_wave_barrier();
       }
-      return;
-    }
-    // Raw sums: each row block (16 x 128 fp32) staged in the wave's slab and written as
-    // 16-byte pieces, 8 store instructions per lane instead of 32 single-float ones.
-    float(*eb)[132] = reinterpret_cast<float(*)[132]>(smem + wave * ER * 132 * 4);
-#pragma unroll
-    for (int i = 0; i < NA; ++i) {
-      const int rb = wave + 4 * i;
-      if (rb >= nrb) break;  // wave-uniform
-#pragma unroll
-      for (int c = 0; c < 4; ++c)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int cl = c * 32 + ((lane & 15) >> 3) * 16 + (lane & 7);
-          eb[4 * (lane >> 4) + e][cl] = acc[i][c][0][e];
-          eb[4 * (lane >> 4) + e][cl + 8] = acc[i][c][1][e];
-        }
-      __builtin_amdgcn_wave_barrier();
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const int rr = 2 * k + (lane >> 5), c4 = 4 * (lane & 31);
-        const int r = rb * 16 + rr;
-        if (r < nrows)
-          *reinterpret_cast<float4*>(pl.y + (size_t)(row0 + r) * pl.ldy + cpg * 128 + c4) =
-              *reinterpret_cast<const float4*>(&eb[rr][c4]);
-      }
-      __builtin_amdgcn_wave_barrier();
+      if (!seq) return;
+      __syncthreads();  // the slabs are the next plane's B buffers
     }
   };
   using std::integral_constant;

@@ -699,7 +699,7 @@ namespace cx {
 
 struct MoeSizes {
   int M, P, n, nsh, chunk, nrb, wpg, max_entries, ntiles;
-  bool small, prefill, tall, mid, down_mid;
+  bool small, prefill, tall, mid, down_mid, tall_mid;
   size_t off_sel, off_wts, off_counts, off_offsets, off_pairs, off_rows, off_inv, off_rexp, off_ent, off_nent, off_tiles;
   size_t off_xg, off_xu, off_yg, off_yu, off_xd, off_yd, off_ysc, total;
 };
@@ -712,6 +712,7 @@ struct PrefillShape {
   int nrb, wpg;
   int kernel;  // prefill GEMM: 0 register-blocked, 1 tall, -1 by the rows per expert
   int mid;     // register-blocked prefill: mid fused into the gate/up GEMM
+  int tall_mid;  // tall prefill: gate, up and the mid in one workgroup, one plane after the other
 };
 PrefillShape PrefillConfig() {
   static const PrefillShape ps = [] {
@@ -722,7 +723,7 @@ PrefillShape PrefillConfig() {
     const int nrb = env("CX_PREFILL_NRB", 4) == 8 ? 8 : 4;
     const int w = env("CX_PREFILL_WPG", 4);
     return PrefillShape{nrb, w == 16 && nrb == 4 ? 16 : w == 4 ? 4 : 8, env("CX_PREFILL_GEMM", -1),
-                        env("CX_PREFILL_MID", 1)};
+                        env("CX_PREFILL_MID", 1), env("CX_TALL_SEQMID", 1)};
   }();
   return ps;
 }
@@ -745,6 +746,7 @@ MoeSizes PlanMoe(const cx_moe_plan* pl, int M, int mode) {
   // Register-blocked prefill: gate and up in one workgroup with the mid fused into the
   // epilogue (64-row entries, 4 waves per plane).
   s.mid = !decode && !s.tall && s.nrb == 4 && ps.mid;
+  s.tall_mid = s.tall && ps.tall_mid;
   // Decode: the mid in the down GEMM's prologue (16 rows of I halves in LDS per workgroup)
   // while at most 128 entries can exist (M (topk + 1) <= 128): the down launch is then at
   // most one generation of workgroups (16 per entry, 8 per CU), and the mid launch it
@@ -878,7 +880,8 @@ bool LaunchExpertGemm(const cx_moe_plan* pl, const MoeSizes& sz, bool gate_up, c
     g.plane[1] = g.plane[0];
   }
   const int ksw = gate_up ? 4 : 1;
-  const int planes = gate_up ? 2 : 1;
+  const int planes = gate_up && !sz.tall_mid ? 2 : 1;
+  g.tall_seq_mid = gate_up && sz.tall_mid;
   const int k2r = gate_up ? pl->k2_gu : pl->k2_d, cbr = gate_up ? pl->cb_gu : pl->cb_d;
   const int k2s = gate_up ? pl->k2_sgu : pl->k2_sd, cbs = gate_up ? pl->cb_sgu : pl->cb_sd;
   const int wpg = g.ncp % sz.wpg == 0 ? sz.wpg : 4;
@@ -1154,7 +1157,7 @@ int MoeForward(const cx_moe_plan* pl, const void* x, int32_t x_dtype, int32_t ld
                         s))
     return CX_E_UNSUPPORTED;
   mark();
-  if (!sz.mid && !sz.down_mid)  // else a GEMM computes the down projection's input rows itself
+  if (!sz.mid && !sz.down_mid && !sz.tall_mid)  // else a GEMM computes the down projection's input rows itself
     hipLaunchKernelGGL(MoeMidKernel, dim3((unsigned)((sz.P + 3) / 4)), dim3(256), 0, s, yg, yu, rexp,
                        pl->tb, M, pl->topk, pl->E, pl->I, xd);
   mark();
