@@ -33,7 +33,7 @@ MFMA_F16_PEAK_TFS = 2500.0  # MI355X dense fp16 MFMA, published (no sparsity)
 E, H, IE, TOPK = 512, 2048, 512, 10
 
 
-GATE_UP_KERNEL = "Exl3GemmKernel<8, 2, 1, 4, 2>"  # the decode gate/up instantiation at 4.0 bpw (mul1)
+GATE_UP_KERNEL = "Exl3GemmKernel<8, 2, 1, 4, 2, false>"  # the decode gate/up instantiation at 4.0 bpw (mul1)
 
 
 def matrix_bytes(i, o, k2):
