@@ -111,12 +111,12 @@ __device__ __forceinline__ void RouteRowWave(const float* __restrict__ lg, int E
   if (lane == 0 && wts_row) wts_row[topk] = Sigmoid(shared);
 }
 
-// One wave per row.
+// One wave per row; blockDim.x / 64 rows per workgroup.
 template <int V>
 __global__ void __launch_bounds__(256) RouteKernel(const float* __restrict__ logits, int ld, int M, int E, int topk,
                                                    const float* __restrict__ shared_logit, int* __restrict__ sel,
                                                    float* __restrict__ wts) {
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int row = blockIdx.x * (int)(blockDim.x >> 6) + (int)(threadIdx.x >> 6);
   if (row >= M) return;  // whole waves leave together
   const float* lg = logits + (size_t)row * ld;
   RouteRowWave<V>(lg, E, topk, shared_logit ? shared_logit[row] : lg[E], sel + (size_t)row * topk,
@@ -825,11 +825,15 @@ void* StaticScratch(hipError_t* err) {
 
 void LaunchRoute(const float* logits, int ld, int M, int E, int topk, const float* shared_logit, int* sel, float* wts,
                  hipStream_t s) {
+  // A row's k rounds are a chain of scalar work (lane reads, ballot counts, branches), and
+  // the CU's scalar unit is shared by its waves: small calls put one routing wave on each
+  // CU.
+  const int wpb = M <= 256 ? 1 : 4;  // waves (rows) per workgroup
+  const dim3 grid((unsigned)((M + wpb - 1) / wpb)), block((unsigned)(64 * wpb));
   if (E <= 512)
-    hipLaunchKernelGGL(RouteKernel<8>, dim3((M + 3) / 4), dim3(256), 0, s, logits, ld, M, E, topk, shared_logit, sel, wts);
+    hipLaunchKernelGGL(RouteKernel<8>, grid, block, 0, s, logits, ld, M, E, topk, shared_logit, sel, wts);
   else
-    hipLaunchKernelGGL(RouteKernel<16>, dim3((M + 3) / 4), dim3(256), 0, s, logits, ld, M, E, topk, shared_logit, sel,
-                       wts);
+    hipLaunchKernelGGL(RouteKernel<16>, grid, block, 0, s, logits, ld, M, E, topk, shared_logit, sel, wts);
 }
 
 // Grouping fused with the input transforms (route-order rows) for small decode calls.
