@@ -120,9 +120,10 @@ struct GemmArgs {
   // (rows at or above xmap_n read row p).  Decode GEMM only.
   const int* xmap;
   int xmap_n;
-  // Prefill gate/up with the mid fused in (Exl3GemmPrefillKernel<..., MID = true>): the
-  // down projection's packed input scales [E + 1][O] and its input rows xd [rows][O] fp16
-  // (MFMA row order), row p at xd + p * O.
+  // Gate/up GEMMs with the mid fused in (Exl3GemmPrefillKernel<..., MID = true>, and the
+  // tall GEMM with tall_seq_mid): the down projection's packed input scales [E + 1][O]
+  // and its input rows xd [rows][O] fp16 (MFMA row order), row p at xd + p * O.  The
+  // decode down GEMM's prologue mid (MIDX) reads mid_suh too.
   const __half* mid_suh;
   __half* mid_xd;
   // Decode down GEMM with the mid in its prologue (Exl3GemmKernel<..., MIDX = true>): the
@@ -808,6 +809,9 @@ namespace cx {
 // row blocks w, w + 4, ... by all 8 column tiles.  So every tile is decoded once per
 // entry of up to 64 NRBW rows, and every activation fragment is loaded by exactly one
 // wave, straight into registers (no activation staging, no sharing needed).
+//
+// tall_seq_mid (gate/up): the workgroup runs the gate plane, then the up plane over the same
+// entry and columns, and computes the mid in the epilogue (grid z = 1).
 //
 // Step pipeline (B fragments in 4 LDS buffers, decode two steps ahead of the MFMAs):
 //   [barrier at even s] | read B(s) | MFMAs of step s, decode of step s + 2 | write B(s + 2)
