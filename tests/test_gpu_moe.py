@@ -174,6 +174,26 @@ def test_tall_prefill_layer(ops, E, k, M, bgu, bd):
     assert e <= 1e-3
 
 
+def test_tall_prefill_mixed_rates(ops):
+    # The shared expert at other rates than the routed ones: each GEMM runs as two launches
+    # (shared entries, then routed), and the tall gate/up launch computes the mid itself in
+    # both.  Every row against the oracle.
+    from exl3moe import synth
+    E, k, M = 4, 2, 300
+    plan = synth.device_moe_layer(41, E=E, H=256, Ie=256, topk=k, bits_gu=3, bits_d=5, shared_bits_gu=4,
+                                  shared_bits_d=6)
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((M, 256)).astype(np.float16)
+    lg = rng.standard_normal((M, E + 1)).astype(np.float32)
+    y, sel, wts = run_layer(plan, x, lg, 2)
+    rs, rw = O.route(lg, E, k)
+    np.testing.assert_array_equal(sel, rs)
+    ref = oracle_layer(plan, x, rs, rw)
+    e = rel_l2(y, ref)
+    print(f"tall mixed rates rel_l2={e:.3e}")
+    assert e <= 1e-3
+
+
 @pytest.mark.parametrize("cb", ["mcg", "3inst"])
 def test_layer_other_codebooks(ops, cb):
     # Every matrix of the layer in the mcg or 3inst codebook: decode, the register-blocked
