@@ -148,6 +148,14 @@ def counters(d: str, out: str, kernels: dict[str, str], cmd: str) -> dict:
             # and as a share of all CU cycles of the launch.
             k["lds_conflict_cycles_per_lds_instruction"] = round(avg["SQ_LDS_BANK_CONFLICT"] / max(1.0, avg["SQ_INSTS_LDS"]), 4)
             k["lds_conflict_frac_of_cu_cycles"] = round(avg["SQ_LDS_BANK_CONFLICT"] / (cycles * CUS), 4)
+        if "SQ_WAVE_CYCLES" in avg:
+            # Where the waves' cycles go (each counter summed over waves, as SQ_WAVE_CYCLES):
+            # waiting on a waitcnt (memory, LDS, ...), waiting to issue (dependencies, a busy
+            # unit), and issuing, per instruction type.
+            wc = max(1.0, avg["SQ_WAVE_CYCLES"])
+            k["wave_cycle_shares"] = {n[3:].lower(): round(avg[n] / wc, 4) for n in (
+                "SQ_WAIT_ANY", "SQ_WAIT_INST_ANY", "SQ_WAIT_INST_LDS", "SQ_ACTIVE_INST_ANY", "SQ_ACTIVE_INST_VALU",
+                "SQ_ACTIVE_INST_LDS", "SQ_ACTIVE_INST_VMEM", "SQ_ACTIVE_INST_SCA", "SQ_ACTIVE_INST_MISC") if n in avg}
         res["kernels"][label] = k
     with open(out, "w") as o:
         json.dump(res, o, indent=1)
