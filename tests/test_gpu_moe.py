@@ -174,6 +174,24 @@ def test_tall_prefill_layer(ops, E, k, M, bgu, bd):
     assert e <= 1e-3
 
 
+def test_smallest_shapes(ops):
+    # H = I = 128 (one Hadamard block, the mid rows' LDS at its minimum) and top-1: decode
+    # with the mid in the down GEMM's prologue (1, 5 rows) and as a launch of its own (60
+    # rows), the register-blocked prefill and the tall prefill, all against the oracle.
+    from exl3moe import synth
+    for E, k, M, mode in ((4, 1, 1, 1), (4, 1, 5, 1), (4, 1, 60, 1), (4, 1, 90, 2), (2, 1, 300, 2)):
+        plan = synth.device_moe_layer(90 + M, E=E, H=128, Ie=128, topk=k)
+        rng = np.random.default_rng(M)
+        x = rng.standard_normal((M, 128)).astype(np.float16)
+        lg = rng.standard_normal((M, E + 1)).astype(np.float32)
+        y, sel, wts = run_layer(plan, x, lg, mode)
+        rs, rw = O.route(lg, E, k)
+        np.testing.assert_array_equal(sel, rs)
+        e = rel_l2(y, oracle_layer(plan, x, rs, rw))
+        print(f"H=I=128 E={E} k={k} M={M} mode={mode} rel_l2={e:.3e}")
+        assert e <= 1e-3
+
+
 def test_tall_prefill_mixed_rates(ops):
     # The shared expert at other rates than the routed ones: each GEMM runs as two launches
     # (shared entries, then routed), and the tall gate/up launch computes the mid itself in
