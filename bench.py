@@ -56,6 +56,7 @@ def parse():
     ap.add_argument("--no-linear", action="store_true", help="skip the config-2 ragged linear measurement")
     ap.add_argument("--no-long", action="store_true", help="skip the config-5 long prefill + output head")
     ap.add_argument("--no-r1", action="store_true", help="skip the R = 1 decode latency measurement")
+    ap.add_argument("--no-router", action="store_true", help="skip the router GEMV measurement")
     ap.add_argument("--no-stream", action="store_true", help="skip the device-copy HBM stream measurement")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--min-warmup-s", type=float, default=0.5,
@@ -294,6 +295,46 @@ def bench_linear(seed, copies=128, warmup=10):
                            "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
                            "rows_per_s": round(float(Ms.sum() / (ms[:, j].sum() / 1000)), 1)}
     del pairs
+    torch.cuda.empty_cache()
+    return out
+
+
+def bench_router(seed, copies=512, calls=256, warmup=16):
+    """The router GEMV with the shared-gate logit (cx_dense_linear, W [E + 1][H] fp16, the
+    engine's fp32 x): decode-sized (24 rows, fp32 products) and config-4-sized (2048 rows,
+    MFMA) calls, rotating over `copies` seeded weight copies (> 1 GiB, cold reads)."""
+    import numpy as np
+    import torch
+    from exl3moe import ops
+    from exl3moe.trace import EventTimer
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    Ws = [torch.randn(E + 1, H, generator=g, device="cuda").half() for _ in range(copies)]
+    out = {"workload": f"router GEMV W [{E + 1}][{H}] fp16, fp32 x, rotating over {copies} weight copies",
+           "copies": copies}
+    for M in (24, 2048):
+        x = torch.randn(M, H, generator=g, device="cuda")
+        y = torch.empty(M, E + 1, dtype=torch.float32, device="cuda")
+        for i in range(warmup):
+            ops.dense_linear(Ws[i % copies], x, y)
+        torch.cuda.synchronize()
+        t = EventTimer(calls, torch.cuda.current_stream().cuda_stream)
+        for i in range(calls):
+            t.mark()
+            ops.dense_linear(Ws[(warmup + i) % copies], x, y)
+        t.mark()
+        us = np.array(t.ms()) * 1000
+        t.close()
+        by = (E + 1) * H * 2 + M * H * 4 + M * (E + 1) * 4
+        med = float(np.median(us))
+        r = {"us": pct(us), "algorithmic_GBps": round(by / (med * 1e-6) / 1e9, 1),
+             "frac_hbm": round(by / (med * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+        if M > 8:
+            tf = 2.0 * M * (E + 1) * H / (med * 1e-6) / 1e12
+            r["TFLOPs"] = round(tf, 1)
+            r["frac_mfma"] = round(tf / MFMA_F16_PEAK_TFS, 4)
+        out[f"M{M}"] = r
+    del Ws
     torch.cuda.empty_cache()
     return out
 
@@ -603,6 +644,8 @@ def main():
         out["decode_r1"] = bench_r1(plans, args.seed + 500)
     if not args.no_linear:
         out["linear"] = bench_linear(args.seed + 300)
+    if not args.no_router:
+        out["router"] = bench_router(args.seed + 600)
     if not args.no_long:
         out["prefill_long"] = bench_long(args.seed + 400)
     if not args.no_stream:
