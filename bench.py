@@ -312,7 +312,7 @@ def bench_router(seed, copies=512, calls=256, warmup=16):
     Ws = [torch.randn(E + 1, H, generator=g, device="cuda").half() for _ in range(copies)]
     out = {"workload": f"router GEMV W [{E + 1}][{H}] fp16, fp32 x, rotating over {copies} weight copies",
            "copies": copies}
-    for M in (24, 2048):
+    for M in (4, 24, 2048):
         x = torch.randn(M, H, generator=g, device="cuda")
         y = torch.empty(M, E + 1, dtype=torch.float32, device="cuda")
         for i in range(warmup):
