@@ -64,3 +64,21 @@ def test_counters_utilisation(tmp_path):
     # 6000 MFMAs x 16384 FLOP in 1000 cycles at 2.4 GHz
     assert abs(k["mfma_issue_TFLOPs"] - 6000 * 16384 / (1000 / 2.4e9) / 1e12) < 0.1
     assert json.loads((tmp_path / "c.json").read_text())["kernels"]["gemm"]["mfma_busy"] == 0.25
+
+
+def test_counters_wave_cycle_shares(tmp_path):
+    # Wave-state counters are divided by SQ_WAVE_CYCLES (same units), per kernel; counters
+    # absent from the run are left out, and another kernel's rows are not mixed in.
+    fields = ["Kernel_Name", "Counter_Name", "Counter_Value"]
+    k = "void cx::G<8>(a)"
+    rows = [{"Kernel_Name": k, "Counter_Name": "GRBM_GUI_ACTIVE", "Counter_Value": 8000},
+            {"Kernel_Name": k, "Counter_Name": "SQ_WAVE_CYCLES", "Counter_Value": 1000},
+            {"Kernel_Name": k, "Counter_Name": "SQ_WAIT_ANY", "Counter_Value": 250},
+            {"Kernel_Name": k, "Counter_Name": "SQ_ACTIVE_INST_VALU", "Counter_Value": 400},
+            {"Kernel_Name": "void cx::Other(a)", "Counter_Name": "GRBM_GUI_ACTIVE", "Counter_Value": 8000},
+            {"Kernel_Name": "void cx::Other(a)", "Counter_Name": "SQ_WAVE_CYCLES", "Counter_Value": 10},
+            {"Kernel_Name": "void cx::Other(a)", "Counter_Name": "SQ_WAIT_ANY", "Counter_Value": 10}]
+    _write(tmp_path / "w" / "run_counter_collection.csv", rows, fields)
+    r = ps.counters(str(tmp_path / "w"), str(tmp_path / "w.json"), {"gemm": "G<8>"}, "cmd")
+    sh = r["kernels"]["gemm"]["wave_cycle_shares"]
+    assert sh == {"wait_any": 0.25, "active_inst_valu": 0.4}
