@@ -386,7 +386,7 @@ int cx_exl3_linear(const cx_exl3_matrix* m, const void* x, int32_t x_dtype, int3
   int rc = CheckMatrix(m);
   if (rc) return rc;
   if (!x || !y || !workspace) return CX_E_ARG;
-  if (M <= 0) return CX_E_SHAPE;
+  if (M <= 0 || !WorkspaceAligned(workspace)) return CX_E_SHAPE;
   if ((rc = RowOffsetsCheck(row_offsets, n_sessions, M))) return rc;
   const cx_exl3_job job{*m, x, x_dtype, ldx, y, y_dtype, m->out_features};
   if ((rc = CheckJob(job))) return rc;
@@ -404,7 +404,7 @@ size_t cx_exl3_group_workspace_size(const cx_exl3_job* jobs, int32_t n_jobs, int
 int cx_exl3_group(const cx_exl3_job* jobs, int32_t n_jobs, int32_t M, const int32_t* row_offsets, int32_t n_sessions,
                   void* workspace, size_t workspace_bytes, cx_stream_t stream) {
   if (!jobs || !workspace) return CX_E_ARG;
-  if (n_jobs <= 0 || n_jobs > kMaxGroupJobs || M <= 0) return CX_E_SHAPE;
+  if (n_jobs <= 0 || n_jobs > kMaxGroupJobs || M <= 0 || !WorkspaceAligned(workspace)) return CX_E_SHAPE;
   int rc;
   for (int j = 0; j < n_jobs; ++j)
     if ((rc = CheckJob(jobs[j]))) return rc;

@@ -12,6 +12,8 @@ namespace cx {
 
 inline bool ValidK2(int k2) { return (k2 >= 2 && k2 <= 16 && !(k2 & 1)) || k2 == 3 || k2 == 5 || k2 == 7; }
 inline size_t AlignUp(size_t v, size_t a) { return (v + a - 1) / a * a; }
+// Workspaces are carved into 256-byte aligned pieces (device tables, 16-byte rows).
+inline bool WorkspaceAligned(const void* p) { return reinterpret_cast<uintptr_t>(p) % 256 == 0; }
 
 inline int LaunchStatus() {
   const hipError_t e = hipGetLastError();

@@ -947,6 +947,7 @@ int cx_moe_group(const int32_t* sel, int32_t M, int32_t E, int32_t topk, int32_t
                  int32_t* pairs, int32_t* row_ids, void* workspace, size_t workspace_bytes, cx_stream_t stream) {
   if (!sel || !counts || !offsets || !pairs || !row_ids) return CX_E_ARG;
   if (M <= 0 || E <= 0 || E > kMaxExperts || topk <= 0 || topk > E) return CX_E_SHAPE;
+  if (workspace && !WorkspaceAligned(workspace)) return CX_E_SHAPE;
   const int n = M * topk;
   const int ntiles = (n + kTile - 1) / kTile;
   if (n > kSmallRoutes && (!workspace || workspace_bytes < cx_moe_group_workspace_size(M, E, topk)))
@@ -1074,6 +1075,7 @@ int MoeForward(const cx_moe_plan* pl, const void* x, int32_t x_dtype, int32_t ld
   if (mode < CX_MOE_AUTO || mode > CX_MOE_PREFILL) return CX_E_ARG;
   if (x_dtype != CX_F16 && x_dtype != CX_F32) return CX_E_ARG;
   if (M <= 0) return CX_E_SHAPE;
+  if (!WorkspaceAligned(workspace) || reinterpret_cast<uintptr_t>(y) % 16) return CX_E_SHAPE;  // y: float4 rows
   // Rows are read in 16- / 32-byte pieces.
   if (ldx < pl->H || ldx % 8 || reinterpret_cast<uintptr_t>(x) % 16) return CX_E_SHAPE;
   if (ld < pl->E || (!shared_logit && ld < pl->E + 1)) return CX_E_SHAPE;

@@ -5,7 +5,8 @@
  * engine's in-process C++: file:line citations are relative to the reference root).
  * All pointers are device pointers unless a parameter says "host".  Every compute call
  * is asynchronous on the given HIP stream, allocates nothing (workspace is caller
- * memory, sized by the matching *_workspace_size query), never exits, and returns:
+ * memory, sized by the matching *_workspace_size query and 256-byte aligned, as hipMalloc
+ * and torch allocations are), never exits, and returns:
  *     0  success
  *    <0  invalid argument or shape (CX_E_*)
  *    >0  a hipError_t from a launch

@@ -65,3 +65,16 @@ def test_argument_errors_without_gpu():
                             ctypes.c_void_p(256), 1 << 30, None) == -2
     assert L.cx_exl3_linear(ctypes.byref(m), ctypes.c_void_p(258), 0, 2048, 4, ro, 2, ctypes.c_void_p(256), 1,
                             ctypes.c_void_p(256), 1 << 30, None) == -2
+
+
+def test_workspace_alignment_checked_without_gpu():
+    # Workspaces are carved into 256-byte aligned pieces: a misaligned one is a shape error,
+    # returned before any launch.
+    import exl3moe
+    L = exl3moe.lib()
+    m = exl3moe.Matrix(1, 1, 1, 2048, 512, 8, 2)
+    ro = exl3moe.i32_host([0, 2, 4])
+    assert L.cx_exl3_linear(ctypes.byref(m), ctypes.c_void_p(256), 0, 2048, 4, ro, 2, ctypes.c_void_p(256), 1,
+                            ctypes.c_void_p(256 + 16), 1 << 30, None) == -2
+    one = ctypes.c_void_p(256)
+    assert L.cx_moe_group(one, 200, 8, 8, one, one, one, one, ctypes.c_void_p(512 + 64), 1 << 30, None) == -2
