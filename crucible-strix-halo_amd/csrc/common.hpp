@@ -164,13 +164,11 @@ __device__ __forceinline__ int WaveMinI(int v) {
              min(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
 }
 
-// Position of input row r (0..15 of a 16-row block) in the MFMA-ordered activation
-// layout.  Lane group q of a 16x16x16 MFMA feeds rows {2q, 2q+1, 2q+8, 2q+9} of a
-// weight tile (the decoder's run layout), so activations are stored as
-// [.., 4q + s, ..] with row(q, s) = 2q + (s & 1) + 8 (s >> 1).
-__host__ __device__ constexpr int PermPos16(int r) { return 4 * ((r & 7) >> 1) + (r & 1) + 2 * (r >> 3); }
+// Input row of slot p (0..15) of one k-tile in the decoder's run layout: lane group q
+// (lanes 16q..16q+15) decodes rows {2q, 2q+1, 2q+8, 2q+9} of a weight tile as slots
+// 4q..4q+3, i.e. row(q, s) = 2q + (s & 1) + 8 (s >> 1) (the dequantizer's element order).
 __host__ __device__ constexpr int PermRow16(int p) { return 2 * (p >> 2) + (p & 1) + 8 * ((p >> 1) & 1); }
-// The same for a 16x16x32 MFMA over two k-tiles (32 input rows): lane group q holds
+// The v_mfma_f32_16x16x32_f16 order over two k-tiles (32 input rows): lane group q holds
 // slots 8q..8q+7 = rows {2q, 2q+1, 2q+8, 2q+9} of the first k-tile, then of the second.
 __host__ __device__ constexpr int PermPos32(int r) { return 8 * ((r & 7) >> 1) + 4 * (r >> 4) + (r & 1) + 2 * ((r >> 3) & 1); }
 __host__ __device__ constexpr int PermRow32(int p) {
