@@ -62,7 +62,22 @@ __device__ __forceinline__ float XorLane(float v) {
 // every nonzero value equals the natural-order network's; an exactly-zero output may
 // carry the other sign of zero.  Callers fold WhtLaneSign() into the scale they apply
 // after the transform (a multiplication by +-1 is exact).
-__device__ __forceinline__ float WhtLaneSign() { return (__builtin_popcount(threadIdx.x & 15) & 1) ? -1.f : 1.f; }
+//
+// Relabelled form (PHI): physical lane L of a 16-lane row holds the elements of lane
+// index e = L ^ 3 when L & 4 (else e = L).  The partners e ^ 1, e ^ 2, e ^ 4, e ^ 8 then
+// sit at physical lanes L ^ 1, L ^ 2, L ^ 7, L ^ 8, one DPP pattern each (the natural
+// layout needs two DPP moves for e ^ 4); signs follow e.  The network and its operands
+// are the same, so are the values.  The caller loads and stores by e
+// (StorePerm32x8LdsBuf<true>).
+__device__ __forceinline__ int PhiLane() {
+  const int L = threadIdx.x & 15;
+  return L ^ (3 * ((L >> 2) & 1));
+}
+template <bool PHI = false>
+__device__ __forceinline__ float WhtLaneSign() {
+  const int e = PHI ? PhiLane() : (threadIdx.x & 15);
+  return (__builtin_popcount(e) & 1) ? -1.f : 1.f;
+}
 
 // In-lane butterfly stages of strides ST0, 2 ST0, ... < 8.
 template <int ST0>
@@ -78,9 +93,10 @@ __device__ __forceinline__ void WhtInLane(float v[8]) {
       }
 }
 
-// Cross-lane stages (strides 8..64) in the signed form.
+// Cross-lane stages (strides 8..64) in the signed form (PHI: the relabelled lanes).
+template <bool PHI = false>
 __device__ __forceinline__ void WhtCrossLaneSigned(float v[8]) {
-  const int j = threadIdx.x & 15;
+  const int j = PHI ? PhiLane() : (threadIdx.x & 15);
   // v_fmac_f32_dpp d, a, s: d += dpp(a) * s.  The compiler does not fold a DPP move into a
   // multiply-add, so the stages are written out; each block starts with the two wait
   // states a DPP read of a just-written VGPR needs.
@@ -107,7 +123,10 @@ __device__ __forceinline__ void WhtCrossLaneSigned(float v[8]) {
     const float sg = (j & 2) ? -1.f : 1.f;
     CX_WHT_STAGE_INPLACE("quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf");
   }
-  {
+  if constexpr (PHI) {
+    const float sg = (j & 4) ? -1.f : 1.f;  // element e ^ 4 is physical lane L ^ 7
+    CX_WHT_STAGE_INPLACE("row_half_mirror row_mask:0xf bank_mask:0xf");
+  } else {
     float a[8];  // lane ^ 4 = (lane ^ 7) ^ 3: the first move by the compiler, the second folded
 #pragma unroll
     for (int i = 0; i < 8; ++i) a[i] = Dpp<kDppRowHalfMirror>(v[i]);
@@ -131,6 +150,7 @@ __device__ __forceinline__ void Wht128x8Signed(float v[8]) {
 // The same transform of 8 fp16 inputs packed in pairs (h[k] = elements 2k, 2k + 1): the
 // stride-1 stage is v_fma_mix_f32 lo * 1 + (+-hi), the fp32 sum of the two values with
 // one rounding, i.e. the conversion to fp32 folded into the first butterfly.
+template <bool PHI = false>
 __device__ __forceinline__ void Wht128x8SignedH(const uint32_t h[4], float v[8]) {
 #pragma unroll
   for (int k = 0; k < 4; ++k)
@@ -139,7 +159,7 @@ __device__ __forceinline__ void Wht128x8SignedH(const uint32_t h[4], float v[8])
         : "=&v"(v[2 * k]), "=v"(v[2 * k + 1])
         : "v"(h[k]));
   WhtInLane<2>(v);
-  WhtCrossLaneSigned(v);
+  WhtCrossLaneSigned<PHI>(v);
 }
 
 
@@ -296,16 +316,19 @@ __device__ __forceinline__ void StorePerm32x8Buf(__amdgpu_buffer_rsrc_t r, uint3
 // wave's 256-dword area (f(q) = (q >> 1) & 3: each of the four writes covers all 32 banks
 // per half wave), then reads its chunk t = s, 16 bytes at 16 q + 4 (t ^ f(q)) (8
 // consecutive lanes cover all banks).  A wave's LDS operations run in order, so no
-// barrier is needed; the area must be the calling wave's own.
+// barrier is needed; the area must be the calling wave's own.  PHI: the lanes hold the
+// relabelled elements (PhiLane), written at their element slot s = e & 3.
+template <bool PHI = false>
 __device__ __forceinline__ void StorePerm32x8LdsBuf(uint32_t* area, __amdgpu_buffer_rsrc_t r, uint32_t voff,
                                                     uint32_t soff, const float v[8], float scale) {
   const int lane = threadIdx.x & 63, j = lane & 15, q = lane >> 2, t = lane & 3, f = (q >> 1) & 3;
+  const int te = PHI ? (PhiLane() & 3) : t;  // the values' lane index within the quad
   uint32_t h[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k)
     h[k] = __builtin_bit_cast(uint32_t, __floats2half2_rn(v[2 * k] * scale, v[2 * k + 1] * scale));
 #pragma unroll
-  for (int k = 0; k < 4; ++k) area[16 * q + 4 * (k ^ f) + t] = h[k];
+  for (int k = 0; k < 4; ++k) area[16 * q + 4 * (k ^ f) + te] = h[k];
   const u32x4_t c = *reinterpret_cast<const u32x4_t*>(area + 16 * q + 4 * (t ^ f));
   __builtin_amdgcn_raw_buffer_store_b128(c, r, voff + (uint32_t)(32 * (j >> 2) + 8 * t) * 2, soff, 0);
 }

@@ -287,6 +287,7 @@ __global__ void __launch_bounds__(1024) GroupSmallKernel(const int* __restrict__
 // The gate and up input transforms of one lane's 8 elements of a 128-block (signed
 // form, before the norm): x, suh_gate, suh_up as 8 packed fp16 each.  RoundH(x * suh) is
 // the fp16 product (an fp16 x fp16 product is exact in fp32, so one fp16 rounding).
+template <bool PHI = false>
 __device__ __forceinline__ void InputPairTransform(const uint4& x, const uint4& sg, const uint4& su, float a[8],
                                                    float v[8]) {
   const uint32_t hx[4] = {x.x, x.y, x.z, x.w};
@@ -298,8 +299,8 @@ __device__ __forceinline__ void InputPairTransform(const uint4& x, const uint4& 
     pa[k] = __builtin_bit_cast(uint32_t, __hmul2(__builtin_bit_cast(__half2, hx[k]), __builtin_bit_cast(__half2, hg[k])));
     pv[k] = __builtin_bit_cast(uint32_t, __hmul2(__builtin_bit_cast(__half2, hx[k]), __builtin_bit_cast(__half2, hu[k])));
   }
-  Wht128x8SignedH(pa, a);
-  Wht128x8SignedH(pv, v);
+  Wht128x8SignedH<PHI>(pa, a);
+  Wht128x8SignedH<PHI>(pv, v);
 }
 
 // Decode: grouping and the gate/up input transforms in one launch, after routing.
@@ -503,7 +504,8 @@ __global__ void __launch_bounds__(256) MoeInputKernel(const void* __restrict__ x
   }
   const __half* sg = tb.gate_suh + (size_t)e * H;
   const __half* su = tb.up_suh + (size_t)e * H;
-  const int g = (threadIdx.x >> 4) & 3, j = threadIdx.x & 15;
+  // Lanes hold relabelled elements (PhiLane): the stride-32 butterfly is one DPP pattern.
+  const int g = (threadIdx.x >> 4) & 3, j = PhiLane();
   const int nb = H / 128, st = 4 * S;
   // Every row touched here is addressed through a buffer resource on its (wave-uniform)
   // start: the lanes' offsets are 32-bit and each block's offset is the uniform soffset,
@@ -543,11 +545,11 @@ __global__ void __launch_bounds__(256) MoeInputKernel(const void* __restrict__ x
       const int blk = b0 + it * st;
       if (blk >= nb) break;  // uniform over the 16-lane group
       float a[8], v[8];
-      InputPairTransform(rx[it], rg[it], ru[it], a, v);
+      InputPairTransform<true>(rx[it], rg[it], ru[it], a, v);
       const uint32_t so = (uint32_t)(it * st * 128) * 2;
       uint32_t* ta = tarea[threadIdx.x >> 6];
-      StorePerm32x8LdsBuf(ta, rdg, (uint32_t)(b0 * 128) * 2, so, a, kHadNorm * WhtLaneSign());
-      StorePerm32x8LdsBuf(ta, rdu, (uint32_t)(b0 * 128) * 2, so, v, kHadNorm * WhtLaneSign());
+      StorePerm32x8LdsBuf<true>(ta, rdg, (uint32_t)(b0 * 128) * 2, so, a, kHadNorm * WhtLaneSign<true>());
+      StorePerm32x8LdsBuf<true>(ta, rdu, (uint32_t)(b0 * 128) * 2, so, v, kHadNorm * WhtLaneSign<true>());
     }
   }
 }
