@@ -34,6 +34,36 @@ E, H, IE, TOPK = 512, 2048, 512, 10
 
 
 GATE_UP_KERNEL = "Exl3GemmKernel<8, 2, 1, 4, 2, false>"  # the decode gate/up instantiation at 4.0 bpw (mul1)
+# The prefill GEMM instantiations this build launches: (profile entry, kernel) per stage.
+PREFILL_KERNELS = {
+    "config4": {"gate_up": ("config 4 gate/up + fused mid", "Exl3GemmPrefillKernel<8, 2, 4, 1, 4, true>"),
+                "down": ("config 4 down", "Exl3GemmPrefillKernel<8, 2, 4, 1, 4, false>")},
+    "config5": {"gate_up": ("config 5 gate/up (3 bpw)", "Exl3GemmTallKernel<6, 2, 3>"),
+                "down": ("config 5 down (5 bpw)", "Exl3GemmTallKernel<10, 2, 3>")},
+}
+
+
+def prefill_traffic(config, stage_us):
+    """HBM bytes per launch of a prefill workload's two GEMMs (FETCH_SIZE + WRITE_SIZE) from
+    the committed counter profile of the same workload, each beside the rate it implies at
+    this run's stage time; None for a stage whose profiled kernel is not the one this build
+    launches (counter collection needs its own rocprofv3 run)."""
+    f = ROOT / "profiles" / "traffic_prefill_gemms_config4_config5.json"
+    try:
+        prof = json.loads(f.read_text())
+    except Exception:
+        return None
+    out = {}
+    for stage, (entry, kernel) in PREFILL_KERNELS[config].items():
+        k = prof.get("kernels", {}).get(entry, {})
+        if k.get("kernel") != kernel:
+            out[stage] = None
+            continue
+        b = int(k["hbm_fetch_bytes_per_launch"]) + int(k["hbm_write_bytes_per_launch"])
+        out[stage] = {"kernel": kernel, "hbm_bytes_per_launch": b,
+                      "GBps_at_stage_time": round(b / (stage_us[stage] * 1e-6) / 1e9, 1)}
+    out["source"] = {"file": "profiles/traffic_prefill_gemms_config4_config5.json", "command": prof.get("command")}
+    return out
 
 
 def matrix_bytes(i, o, k2):
@@ -363,6 +393,7 @@ def bench_long(seed, steps=3, head_copies=5, head_calls=20):
                     "frac_layer": round(flops / (ms / 1000) / 1e12 / MFMA_F16_PEAK_TFS, 4)},
            "stage_us_mean": {n: round(float(st[:, i].mean() * 1000), 2) for i, n in enumerate(
                ["route", "group", "input", "gate_up", "mid", "down", "combine"])}}
+    out["traffic"] = prefill_traffic("config5", out["stage_us_mean"])
     gen = torch.Generator(device="cuda")
     gen.manual_seed(seed + 1)
     heads = []
@@ -640,6 +671,7 @@ def main():
             "stage_us_mean": {n: round(float(stp[:, i].mean() * 1000), 2) for i, n in enumerate(
                 ["route", "group", "input", "gate_up", "mid", "down", "combine"])},
         }
+        out["prefill"]["traffic"] = prefill_traffic("config4", out["prefill"]["stage_us_mean"])
     if not args.no_r1:
         out["decode_r1"] = bench_r1(plans, args.seed + 500)
     if not args.no_linear:
