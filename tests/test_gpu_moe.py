@@ -214,10 +214,11 @@ def test_tall_prefill_mixed_rates(ops):
 
 @pytest.mark.parametrize("cb", ["mcg", "3inst"])
 def test_layer_other_codebooks(ops, cb):
-    # Every matrix of the layer in the mcg or 3inst codebook: decode, the register-blocked
-    # prefill GEMM (fused mid) and the tall prefill GEMM, against the oracle.
+    # Every matrix of the layer in the mcg or 3inst codebook: decode (4 rows: the mid in the
+    # down GEMM's prologue; 40 rows: the mid launch), the register-blocked prefill GEMM
+    # (fused mid) and the tall prefill GEMM, against the oracle.
     from exl3moe import synth
-    for E, k, M, mode in ((16, 4, 40, 1), (16, 4, 40, 2), (8, 2, 500, 2)):
+    for E, k, M, mode in ((16, 4, 4, 1), (16, 4, 40, 1), (16, 4, 40, 2), (8, 2, 500, 2)):
         plan = synth.device_moe_layer(70 + E, E=E, H=256, Ie=256, topk=k, codebook=cb)
         rng = np.random.default_rng(M + mode)
         x = rng.standard_normal((M, 256)).astype(np.float16)
