@@ -179,7 +179,9 @@ def graph_decode(plans, batches, warmup, steps, mode):
     """The same decode steps captured in one HIP graph (the layer records only kernel
     launches, no allocations or memsets) and replayed: the device time of the layer chain
     without the host launch cost, as a serving loop that captures one graph per batch
-    shape sees it.  Returns ms per step (best of 3 replays) or None."""
+    shape sees it.  The graph holds at least 200 steps (a replay has a fixed start-up cost
+    that shorter graphs do not amortize).  Returns (ms per step, best of 3 replays, steps in
+    the graph) or None."""
     import numpy as np
     import torch
     from exl3moe.trace import EventTimer
@@ -192,6 +194,7 @@ def graph_decode(plans, batches, warmup, steps, mode):
         offs, x, lg = batches[i % len(batches)]
         plans[i % len(plans)](x, lg, row_offsets=offs, mode=mode, workspace=ws, y=ys[:offs[-1]],
                               sel=sels[i % len(batches)])
+    steps = max(steps, 200)
     try:
         for i in range(warmup):
             call(i)
@@ -210,7 +213,7 @@ def graph_decode(plans, batches, warmup, steps, mode):
         ms = float(np.min(tg.ms())) / steps
         tg.close()
         del gr
-        return ms
+        return ms, steps
     except RuntimeError as e:  # capture unsupported: report eager numbers only
         print(f"bench.py: graph capture of the decode steps failed: {e}", file=sys.stderr)
         return None
@@ -502,6 +505,71 @@ def _cpu_model() -> str:
     return "unknown"
 
 
+def _oracle_step(plan, xh, sel, wts):
+    """A callable running one whole layer call through the oracle on the host: decode of the
+    distinct routed experts' weights + the shared expert's, then the layer math over every
+    row.  The weights leave the GPU before; the callable returns its own duration."""
+    import numpy as np
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle as O
+    used = sorted(set(sel.ravel().tolist()))
+
+    def host(t):
+        return (t.cpu().numpy() if hasattr(t, "cpu") else t).view(np.uint16)
+
+    raw = {e: {k: (host(plan._experts[e][k].trellis), plan._experts[e][k]) for k in ("gate", "up", "down")}
+           for e in used}
+    sh_raw = {k: (host(plan._shared[k].trellis), plan._shared[k]) for k in ("gate", "up", "down")}
+    scales = {id(lin): (lin.suh.cpu().numpy(), lin.svh.cpu().numpy())
+              for d in list(raw.values()) + [sh_raw] for _, lin in d.values()}
+
+    def dec3(d):
+        out = {}
+        for n, key in (("g", "gate"), ("u", "up"), ("d", "down")):
+            tr, lin = d[key]
+            out["w" + n] = O.reconstruct_inner(tr, lin.k2 / 2, lin.codebook)
+            out["s" + n], out["v" + n] = scales[id(lin)]
+        return out
+
+    def one_step():
+        t1 = time.perf_counter()
+        experts = {e: dec3(raw[e]) for e in used}
+        shd = dec3(sh_raw)
+        dummy = experts[used[0]]
+        O.moe_layer([experts.get(e, dummy) for e in range(E)], shd, xh, sel, wts)
+        return time.perf_counter() - t1
+
+    return one_step, len(used)
+
+
+def cpu_baseline_prefill(plan, batch, seconds):
+    """The oracle over one whole config-4 prefill call (2048 rows, Zipf-skewed routing) on the
+    host cores: decode of every routed expert's weights + the layer math over all rows, no
+    subset and no scaling.  One untimed warm-up call, then timed calls while they fit in
+    `seconds` (at least one); the median is reported."""
+    import numpy as np
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle as O
+    offs, x, lg = batch
+    xh = x.cpu().numpy()
+    sel, wts = O.route(lg.cpu().numpy(), E, TOPK)
+    one_step, n_used = _oracle_step(plan, xh, sel, wts)
+    threads = O.num_threads()
+    t0 = time.perf_counter()
+    one_step()
+    runs = [one_step()]
+    while time.perf_counter() - t0 + runs[-1] < seconds and len(runs) < 5:
+        runs.append(one_step())
+    med = float(np.median(runs))
+    rows = xh.shape[0]
+    return {"value": round(rows / med, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "cpu_model": _cpu_model(), "omp_threads": threads, "runs": len(runs),
+            "step_s": {"median": round(med, 4), "min": round(min(runs), 4), "max": round(max(runs), 4)},
+            "sample": f"one whole config-4 prefill call of {rows} rows ({n_used} distinct routed experts + the "
+                      f"shared one): host decode of their weights + the layer math over every row "
+                      f"(oracle/exl3_oracle.c, OpenMP); median of {len(runs)} timed calls after one warm-up call"}
+
+
 def cpu_baseline(plan, batch, seconds):
     """The oracle (C restatement, OpenMP) on the host cores over whole decode steps of the
     same workload: decode of the routed experts' weights + the layer math.  One untimed
@@ -514,36 +582,8 @@ def cpu_baseline(plan, batch, seconds):
     xh = x.cpu().numpy()
     lgh = lg.cpu().numpy()
     sel, wts = O.route(lgh, E, TOPK)
-    used = sorted(set(sel.ravel().tolist()))
-
-    def host(t):
-        return (t.cpu().numpy() if hasattr(t, "cpu") else t).view(np.uint16)
-
     # Weights leave the GPU before any clock starts; decode + math is timed.
-    raw = {e: {k: (host(plan._experts[e][k].trellis), plan._experts[e][k]) for k in ("gate", "up", "down")}
-           for e in used}
-    sh_raw = {k: (host(plan._shared[k].trellis), plan._shared[k]) for k in ("gate", "up", "down")}
-
-    def one_step():
-        t1 = time.perf_counter()
-
-        def dec(tr, lin):
-            return {"w": O.reconstruct_inner(tr, lin.k2 / 2, lin.codebook), "s": lin.suh.cpu().numpy(),
-                    "v": lin.svh.cpu().numpy()}
-        experts = {}
-        for e in used:
-            d = {}
-            for n, key in (("g", "gate"), ("u", "up"), ("d", "down")):
-                p = dec(*raw[e][key])
-                d["w" + n], d["s" + n], d["v" + n] = p["w"], p["s"], p["v"]
-            experts[e] = d
-        shd = {}
-        for n, key in (("g", "gate"), ("u", "up"), ("d", "down")):
-            p = dec(*sh_raw[key])
-            shd["w" + n], shd["s" + n], shd["v" + n] = p["w"], p["s"], p["v"]
-        dummy = experts[used[0]]
-        O.moe_layer([experts.get(e, dummy) for e in range(E)], shd, xh, sel, wts)
-        return time.perf_counter() - t1
+    one_step, n_used = _oracle_step(plan, xh, sel, wts)
 
     threads = O.num_threads()
     t_start = time.perf_counter()
@@ -564,7 +604,7 @@ def cpu_baseline(plan, batch, seconds):
             "omp_threads": threads, "runs": len(runs),
             "step_s": {"median": round(med, 4), "min": round(min(runs), 4), "max": round(max(runs), 4)},
             "single_thread": {"value": round(rows / single, 3), "unit": "tokens/s", "step_s": round(single, 3)},
-            "sample": f"config-3 decode step of {rows} rows ({len(used)} distinct routed experts + the shared one): "
+            "sample": f"config-3 decode step of {rows} rows ({n_used} distinct routed experts + the shared one): "
                       f"host decode of their weights + the layer math (oracle/exl3_oracle.c, OpenMP); median of "
                       f"{len(runs)} timed steps after one warm-up step, then one step on 1 thread"}
 
@@ -649,9 +689,11 @@ def main():
                   "stage_us_mean": {n: round(float(st[:, i].mean() * 1000), 2) for i, n in enumerate(
                       ["route", "group", "input", "gate_up", "mid", "down", "combine"])}},
     }
-    gms = graph_decode(plans, batches, args.warmup, args.steps, CX_MOE_DECODE)
-    if gms is not None:
-        out["graph"] = {"tokens_per_s": round(r["rows"] / (gms * args.steps / 1000), 1), "ms_per_step": round(gms, 4)}
+    g = graph_decode(plans, batches, args.warmup, args.steps, CX_MOE_DECODE)
+    if g is not None:
+        gms, gsteps = g
+        out["graph"] = {"tokens_per_s": round(r["rows"] / (gms * args.steps / 1000), 1), "ms_per_step": round(gms, 4),
+                        "steps_in_graph": gsteps}
     if not args.no_prefill:
         pb = make_batches(2, args.seed + 200, prefill=True)
         rp = run_workload(plans, pb, 2, args.prefill_steps, CX_MOE_PREFILL, args.min_warmup_s)
@@ -684,6 +726,8 @@ def main():
         out["roofline"]["measured_stream_GBps"] = stream_peak()
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(plans[0], batches[0], args.cpu_seconds)
+        if not args.no_prefill:
+            out["prefill"]["cpu_baseline"] = cpu_baseline_prefill(plans[0], pb[0], args.cpu_seconds)
     print(json.dumps(out), flush=True)
 
 

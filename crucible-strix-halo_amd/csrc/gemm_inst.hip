@@ -24,6 +24,8 @@ bool CX_CAT(LaunchGemmRate, CX_RATE)(int cb, int nrb, int ksw, dim3 grid, const 
         hipLaunchKernelGGL((Exl3GemmKernel<K2, CB, NRB, KSW, U, true>), grid, dim3(256), lds, s, g);
         return true;
       }
+    } else if (g.mid_yg) {
+      return false;  // the prologue mid exists for one row block per wave and no K split only
     }
     hipLaunchKernelGGL((Exl3GemmKernel<K2, CB, NRB, KSW, U>), grid, dim3(256), 0, s, g);
     return true;

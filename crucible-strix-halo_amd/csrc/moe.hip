@@ -681,6 +681,37 @@ __global__ void __launch_bounds__(256) MoeCombineKernel(const void* __restrict__
   }
 }
 
+// Environment switches (the defaults are the measured best), read when a plan is created
+// and kept in it, so each plan runs one fixed configuration:
+//   CX_PREFILL_NRB (4 | 8) and CX_PREFILL_WPG (4 | 8 | 16): a register-blocked prefill
+//     workgroup of wpg waves covers 16 nrb rows x 32 wpg columns;
+//   CX_PREFILL_GEMM: 0 register-blocked, 1 tall, -1 by the rows per expert;
+//   CX_PREFILL_MID: the mid fused into the register-blocked gate/up GEMM (needs nrb = 4);
+//   CX_TALL_SEQMID: tall prefill with gate, up and the mid in one workgroup, one plane after
+//     the other (0: separate plane workgroups and a mid launch);
+//   CX_DOWN_MID: -1 the decode mid in the down GEMM's prologue at M (topk + 1) <= 128, 0 / 1
+//     never / always (I <= 1024);
+//   CX_FUSED_ROUTE: -1 routing inside the grouping launch at M <= 16, 0 / 1 never / for every
+//     small call.
+struct Switches {
+  int nrb, wpg;
+  int kernel;
+  int mid;
+  int tall_mid;
+  int down_mid;
+  int fused_route;
+};
+inline Switches ReadSwitches() {
+  auto env = [](const char* k, int d) {
+    const char* e = std::getenv(k);
+    return e ? std::atoi(e) : d;
+  };
+  const int nrb = env("CX_PREFILL_NRB", 4) == 8 ? 8 : 4;
+  const int w = env("CX_PREFILL_WPG", 4);
+  return Switches{nrb, w == 16 && nrb == 4 ? 16 : w == 4 ? 4 : 8, env("CX_PREFILL_GEMM", -1), env("CX_PREFILL_MID", 1),
+                  env("CX_TALL_SEQMID", 1), env("CX_DOWN_MID", -1), env("CX_FUSED_ROUTE", -1)};
+}
+
 }  // namespace cx
 
 // ---- plan ----------------------------------------------------------------------------------
@@ -694,7 +725,8 @@ struct cx_moe_plan {
   cx::ExpertTables tb;
   hipEvent_t* trace;                 // caller's events (nullable), recorded between stages
   int n_trace, trace_cursor;
-  void* scratch;                     // this device's address of the library's static scratch
+  void* scratch;                     // this device's address of the library's static scratch (nullable)
+  cx::Switches sw;                   // environment switches, read when the plan is created
 };
 
 namespace cx {
@@ -706,30 +738,6 @@ struct MoeSizes {
   size_t off_xg, off_xu, off_yg, off_yu, off_xd, off_yd, off_ysc, total;
 };
 
-// Prefill GEMM shape: a workgroup of wpg waves covers 16 nrb rows x 32 wpg columns (every
-// row of an entry shares each decoded tile, every wave of the workgroup shares the
-// activation tiles).  Environment overrides: CX_PREFILL_NRB (4 | 8), CX_PREFILL_WPG
-// (4 | 8 | 16).
-struct PrefillShape {
-  int nrb, wpg;
-  int kernel;  // prefill GEMM: 0 register-blocked, 1 tall, -1 by the rows per expert
-  int mid;     // register-blocked prefill: mid fused into the gate/up GEMM
-  int tall_mid;  // tall prefill: gate, up and the mid in one workgroup, one plane after the other
-};
-PrefillShape PrefillConfig() {
-  static const PrefillShape ps = [] {
-    auto env = [](const char* k, int d) {
-      const char* e = std::getenv(k);
-      return e ? std::atoi(e) : d;
-    };
-    const int nrb = env("CX_PREFILL_NRB", 4) == 8 ? 8 : 4;
-    const int w = env("CX_PREFILL_WPG", 4);
-    return PrefillShape{nrb, w == 16 && nrb == 4 ? 16 : w == 4 ? 4 : 8, env("CX_PREFILL_GEMM", -1),
-                        env("CX_PREFILL_MID", 1), env("CX_TALL_SEQMID", 1)};
-  }();
-  return ps;
-}
-
 MoeSizes PlanMoe(const cx_moe_plan* pl, int M, int mode) {
   MoeSizes s{};
   s.M = M;
@@ -737,7 +745,7 @@ MoeSizes PlanMoe(const cx_moe_plan* pl, int M, int mode) {
   s.P = s.n + M;
   const bool decode = mode == CX_MOE_DECODE || (mode == CX_MOE_AUTO && M <= 64);
   s.prefill = !decode;
-  const PrefillShape ps = PrefillConfig();
+  const Switches& ps = pl->sw;
   s.nrb = decode ? 1 : ps.nrb;
   s.wpg = decode ? 4 : ps.wpg;
   // The tall GEMM when experts average at least 96 rows (one decode then serves up to 192
@@ -754,13 +762,9 @@ MoeSizes PlanMoe(const cx_moe_plan* pl, int M, int mode) {
   // most one generation of workgroups (16 per entry, 8 per CU), and the mid launch it
   // saves is pure latency.  Measured on config 3: -2 to -2.5 us per layer at 1-8 rows, no
   // change at 12-32, +2 to +4 us at 40 (every workgroup recomputes its entry's mid).
-  // Environment override: CX_DOWN_MID = 0 / 1 forces it off / on (decode, I <= 1024).
-  static const int down_mid_env = [] {
-    const char* e = std::getenv("CX_DOWN_MID");
-    return e ? std::atoi(e) : -1;
-  }();
+  // Switch CX_DOWN_MID = 0 / 1 forces it off / on (decode, I <= 1024).
   s.down_mid = decode && pl->I <= 1024 &&
-               (down_mid_env < 0 ? (long)M * (pl->topk + 1) <= 128 : down_mid_env != 0);
+               (ps.down_mid < 0 ? (long)M * (pl->topk + 1) <= 128 : ps.down_mid != 0);
   // Decode: one 16-row block per entry; prefill: every row of an entry shares each decoded tile.
   s.chunk = 16 * s.nrb;
   s.nsh = (M + s.chunk - 1) / s.chunk;
@@ -1041,13 +1045,14 @@ int cx_moe_plan_create(const cx_moe_layer* layer, cx_moe_plan** out) {
     return (int)err;
   }
   pl->tb = ExpertTables{pl->d_tables, pl->d_tables + n, pl->d_tables + 2 * n, g_suh, u_suh, g_svh, u_svh, d_suh};
+  // The static scratch serves only cx_moe_layer_forward_static: a failed lookup leaves it
+  // null (that entry point then returns CX_E_ARG) and does not fail the plan.
   pl->scratch = StaticScratch(&err);
   if (err != hipSuccess) {
-    (void)hipFree(pl->d_scales);
-    (void)hipFree(pl->d_tables);
-    delete pl;
-    return (int)err;
+    pl->scratch = nullptr;
+    (void)hipGetLastError();
   }
+  pl->sw = ReadSwitches();
   *out = pl;
   return CX_OK;
 }
@@ -1118,11 +1123,7 @@ int MoeForward(const cx_moe_plan* pl, const void* x, int32_t x_dtype, int32_t ld
   const bool front = !sz.prefill && FrontEndFits(M, pl->E, pl->topk);
   // Routing fused into the grouping launch when workgroup 0 routes every row in one round
   // of its 16 waves (M <= 16; CX_FUSED_ROUTE = 0 / 1 forces it off / on for any small call).
-  static const int fused_route_env = [] {
-    const char* e = std::getenv("CX_FUSED_ROUTE");
-    return e ? std::atoi(e) : -1;
-  }();
-  const bool fused_route = fused_route_env < 0 ? M <= 16 : fused_route_env != 0;
+  const bool fused_route = pl->sw.fused_route < 0 ? M <= 16 : pl->sw.fused_route != 0;
   if (front && fused_route) {
     // Routing, grouping and input transforms in one launch; the trace records it as the
     // route stage (group and input stages empty).

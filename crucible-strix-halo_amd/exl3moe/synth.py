@@ -26,13 +26,17 @@ def sessions(rng, n: int, lo: int, hi: int) -> list[int]:
     return [0] + np.cumsum(sizes).tolist()
 
 
-def zipf_bias(rng, E: int, s: float = 1.1, scale: float = 0.23) -> np.ndarray:
-    """Per-expert router bias from Zipf(s) rank weights (a random expert order), scaled so
-    expert token counts are skewed: at 2048 tokens and top-10 the heaviest expert gets
-    about 400 tokens and the lightest about 10."""
-    ranks = rng.permutation(E) + 1
-    w = ranks.astype(np.float64) ** (-s)
-    return (scale * np.log(w / w.mean())).astype(np.float32)
+def zipf_bias(rng, E: int, s: float = 1.1, scale: float = 0.23, tail: float = 4.0, knee: float = 0.75) -> np.ndarray:
+    """Per-expert router bias from Zipf(s) rank weights (a random expert order): expert token
+    counts are skewed from 0 to about 400 at 2048 tokens and top-10.
+
+    scale * log(w / mean w) with w = rank^-s sets the head (the heaviest expert gets ~400-460
+    tokens); the ranks past knee * E fall off faster by tail * log(rank / (knee E)), so the
+    coldest experts get no tokens at all (~15-20 of 512 at 2048 tokens)."""
+    ranks = (rng.permutation(E) + 1).astype(np.float64)
+    w = ranks ** (-s)
+    b = scale * np.log(w / w.mean()) - tail * np.log(np.maximum(ranks / (knee * E), 1.0))
+    return b.astype(np.float32)
 
 
 def device_linear(gen, I: int, O: int, bits: float, device="cuda", codebook: str = "mul1"):

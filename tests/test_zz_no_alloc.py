@@ -32,25 +32,43 @@ def _static(L, plan, x, lg, mode, y, sel, wts, offs=None):
         exl3moe.stream_ptr())
 
 
-@pytest.mark.parametrize("E,H,Ie,k,sizes,mode", [
-    (512, 2048, 512, 10, (40, 7), 1),   # config 3 shape, decode
-    (16, 256, 128, 4, (300, 33), 2),    # small layer, prefill plan
+def _sessions(M, rng):
+    """Ragged session offsets over M rows (1 to 5 rows per session)."""
+    cuts = [0]
+    while cuts[-1] < M:
+        cuts.append(min(M, cuts[-1] + int(rng.integers(1, 6))))
+    return cuts
+
+
+@pytest.mark.parametrize("E,H,Ie,k,sizes,mode,xf32", [
+    (512, 2048, 512, 10, (40, 7), 1, False),   # config 3 shape, decode
+    (16, 256, 128, 4, (300, 33), 2, False),    # small layer, prefill plan
+    # fp32 residual rows with a padded row stride and ragged session offsets (the
+    # engine's x_ form of the call), decode and prefill
+    (512, 2048, 512, 10, (24, 5), 1, True),
+    (16, 256, 128, 4, (300, 33), 2, True),
 ])
-def test_static_matches_workspace_entry(lib, E, H, Ie, k, sizes, mode):
+def test_static_matches_workspace_entry(lib, E, H, Ie, k, sizes, mode, xf32):
     from exl3moe import synth
     plan = synth.device_moe_layer(3 if E == 512 else 11, E=E, H=H, Ie=Ie, topk=k)
     rng = np.random.default_rng(E + mode)
     for M in sizes:
-        print(f"static entry: E={E} M={M} mode={mode}", flush=True)
-        x = torch.from_numpy(rng.standard_normal((M, H)).astype(np.float16)).cuda()
+        print(f"static entry: E={E} M={M} mode={mode} fp32 x={xf32}", flush=True)
+        if xf32:
+            xs = torch.from_numpy(rng.standard_normal((M, H + 64)).astype(np.float32)).cuda()
+            x = xs[:, :H]  # ldx = H + 64
+            offs = _sessions(M, rng)
+        else:
+            x = torch.from_numpy(rng.standard_normal((M, H)).astype(np.float16)).cuda()
+            offs = None
         lg = torch.from_numpy(rng.standard_normal((M, E + 1)).astype(np.float32)).cuda()
         sel0 = torch.empty(M, k, dtype=torch.int32, device="cuda")
         wts0 = torch.empty(M, k + 1, dtype=torch.float32, device="cuda")
-        want = plan(x, lg, mode=mode, sel=sel0, wts=wts0)
+        want = plan(x, lg, mode=mode, sel=sel0, wts=wts0, row_offsets=offs)
         y = torch.full((M, H), float("nan"), device="cuda")
         sel = torch.empty_like(sel0)
         wts = torch.empty_like(wts0)
-        assert _static(lib, plan, x, lg, mode, y, sel, wts) == 0
+        assert _static(lib, plan, x, lg, mode, y, sel, wts, offs) == 0
         torch.cuda.synchronize()
         assert torch.equal(y.view(torch.int32), want.view(torch.int32))
         assert torch.equal(sel, sel0) and torch.equal(wts.view(torch.int32), wts0.view(torch.int32))
