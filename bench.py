@@ -33,7 +33,14 @@ MFMA_F16_PEAK_TFS = 2500.0  # MI355X dense fp16 MFMA, published (no sparsity)
 E, H, IE, TOPK = 512, 2048, 512, 10
 
 
-GATE_UP_KERNEL = "Exl3GemmKernel<8, 2, 1, 4, 2, false>"  # the decode gate/up instantiation at 4.0 bpw (mul1)
+STAGE_KERNEL = "Exl3DecodeStageKernel<8, 2>"  # gate/up + mid + down of a decode call in one launch (4.0 bpw, mul1)
+
+
+def uses_stage(M):
+    """Whether the library runs a config-3 decode call of M rows as one stage launch (gate/up,
+    mid and down): M (topk + 1) above 128 (below, the down GEMM computes the mid in its
+    prologue), M <= 64, and CX_STAGE not 0 (csrc/moe.hip PlanMoe)."""
+    return os.environ.get("CX_STAGE", "1") != "0" and M * (TOPK + 1) > 128 and M <= 64
 # The prefill GEMM instantiations this build launches: (profile entry, kernel) per stage.
 PREFILL_KERNELS = {
     "config4": {"gate_up": ("config 4 gate/up + fused mid", "Exl3GemmPrefillKernel<8, 2, 4, 1, 4, true>"),
@@ -637,13 +644,19 @@ def main():
     ms_step = r["wall_s"] * 1000 / args.steps
     tok_s = r["rows"] / r["wall_s"]
     st = np.array(r["stages"])  # [steps][7] ms
+    # The dominant kernel: the decode stage launch (gate/up, mid and down in one kernel; its
+    # trace interval is the gate/up stage, the mid and down intervals hold no kernel).
+    # Algorithmic bytes per launch: the distinct routed experts' + the shared expert's gate,
+    # up and down weights (tiles + scales), the gate/up inputs it reads (xg, xu fp16) and the
+    # down output rows it writes (fp32); the gate/up sums and the mid rows it passes between
+    # its workgroups inside one XCD's L2 are not counted.  Steps whose row count runs the
+    # GEMMs as separate launches (few rows) are left out of it.
+    sm = np.array([uses_stage(m) for m in r["M"]])
+    P = np.array([m * TOPK + m for m in r["M"]])
+    dist = np.array(r["distinct"])
+    kb = (dist + 1) * eb + P * H * 2 * 2 + P * H * 4
     gu = st[:, 3]
-    # Algorithmic bytes of the gate/up launch: distinct routed experts' + shared gate/up
-    # weights (tiles + scales) + its activations (xh in, fp32 out) per step.
-    gu_w = 2 * matrix_bytes(H, IE, k2)
-    P = [m * TOPK + m for m in r["M"]]
-    gu_bytes = np.array([(u + 1) * gu_w + p * H * 2 * 2 + p * IE * 4 * 2 for u, p in zip(r["distinct"], P)])
-    gu_achieved = float(gu_bytes.sum() / (gu.sum() / 1000)) / 1e9
+    stage_achieved = float(kb[sm].sum() / (gu[sm].sum() / 1000)) / 1e9 if sm.any() else 0.0
     layer_bytes = np.array([(u + 1) * eb + m * H * 2 + m * H * 4 + m * (E + 1) * 4 for u, m in zip(r["distinct"], r["M"])])
     layer_gbs = float(layer_bytes.sum() / r["wall_s"]) / 1e9
     # HBM bytes per gate/up launch: not measurable inside this run (counter collection needs
@@ -651,13 +664,13 @@ def main():
     # with its provenance beside it (traffic_source), and dropped when the profile names
     # another kernel instantiation than the one this build launches.
     traffic, traffic_src = None, None
-    tf = ROOT / "profiles" / "traffic_decode_gate_up.json"
+    tf = ROOT / "profiles" / "traffic_decode_stage.json"
     if tf.exists():
         try:
             tj = json.loads(tf.read_text())
-            if tj.get("kernel") == GATE_UP_KERNEL:
+            if tj.get("kernel") == STAGE_KERNEL:
                 traffic = tj.get("hbm_bytes_per_launch")
-                traffic_src = {"file": "profiles/traffic_decode_gate_up.json", "kernel": tj.get("kernel"),
+                traffic_src = {"file": "profiles/traffic_decode_stage.json", "kernel": tj.get("kernel"),
                                "command": tj.get("command"), "note": "measured by rocprofv3 --pmc in a separate "
                                "run of this bench workload, FETCH_SIZE scaled by a device-copy calibration"}
         except Exception:
@@ -680,10 +693,12 @@ def main():
                                "8 ragged sessions x 1..5 rows",
                    "layers_rotated": args.layers, "rows_per_step_mean": round(float(np.mean(r["M"])), 2),
                    "distinct_experts_mean": round(float(np.mean(r["distinct"])), 1)},
-        "roofline": {"bound": "hbm", "kernel": "Exl3GemmKernel (gate/up)", "achieved": round(gu_achieved, 1),
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gu_achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic, "traffic_source": traffic_src, "avg_us": round(float(gu.mean() * 1000), 2),
-                     "algorithmic_bytes_per_launch": int(gu_bytes.mean())},
+        "roofline": {"bound": "hbm", "kernel": "Exl3DecodeStageKernel (gate/up, mid, down)",
+                     "achieved": round(stage_achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(stage_achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_source": traffic_src,
+                     "avg_us": round(float(gu[sm].mean() * 1000), 2) if sm.any() else None,
+                     "algorithmic_bytes_per_launch": int(kb[sm].mean()) if sm.any() else None,
+                     "launches": int(sm.sum())},
         "layer": {"algorithmic_GBps": round(layer_gbs, 1), "frac_hbm": round(layer_gbs / HBM_PEAK_GBS, 4),
                   "traced_step_us": pct(st.sum(1) * 1000),
                   "stage_us_mean": {n: round(float(st[:, i].mean() * 1000), 2) for i, n in enumerate(

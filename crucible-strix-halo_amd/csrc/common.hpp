@@ -301,6 +301,14 @@ __device__ __forceinline__ u32x2_t BufLoad64(__amdgpu_buffer_rsrc_t r, uint32_t 
 __device__ __forceinline__ u32x4_t BufLoad128(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
 }
+// Loads with the device-scope (sc1) cache policy: they miss in the CU's L1 and read the
+// XCD's L2, so they see what other workgroups on the same XCD stored with plain stores and
+// published (stores acknowledged, then an agent-scope flag) during the same launch.  The L2
+// of another XCD is not coherent with it: such data must stay on one XCD.
+constexpr int kPolicyL2 = 16;  // sc1
+__device__ __forceinline__ u32x4_t BufLoad128L2(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, kPolicyL2);
+}
 // The same store through a buffer resource: the block at byte offset voff + soff (voff may
 // differ per lane group, soff is uniform), the lane's chunk at + (32 (j >> 2) + 8 t) * 2.
 __device__ __forceinline__ void StorePerm32x8Buf(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,

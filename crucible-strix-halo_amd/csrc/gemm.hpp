@@ -103,6 +103,10 @@ __device__ __forceinline__ void StoreBlockRow(const GemmPlane& pl, size_t row, i
   if ((threadIdx.x & 15) == 0) pl.ysc[row * (O / 128) + c0 / 128] = ldexpf(1.f, sh);
 }
 
+// Counters of the decode stage launch, one per 128-byte line (the waiting workgroups' polls
+// of one entry do not share a line with another entry's arrivals).
+constexpr int kStageCtrStride = 32;
+
 struct GemmArgs {
   GemmPlane plane[2];
   const int4* entries;   // {matrix, row0, nrows, unused}; nullptr: dense rows (below)
@@ -138,6 +142,12 @@ struct GemmArgs {
   // parks its raw sums in plane 0's y, runs plane 1 (up) and computes the mid of its rows
   // into mid_xd from the parked gate sums and the up sums in registers.
   int tall_seq_mid;
+  // Decode stage launch (Exl3DecodeStageKernel): per row entry a counter, zero at launch;
+  // each gate/up workgroup adds 1 after its sums are stored (stage_arrivals of them), the
+  // last one computes the entry's mid and adds 1 more; the entry's down workgroups wait for
+  // stage_arrivals + 1.
+  int* stage_ctr;  // entry e's counter at stage_ctr[e * kStageCtrStride]
+  int stage_arrivals;
 };
 
 // The mid of one row's 128-column block on 16 lanes (lane j: columns c0 + 8j..8j+7): the
@@ -172,6 +182,48 @@ __device__ __forceinline__ void MidBlock(float gv[8], float uv[8], const __half*
   float v[8];
   MidValues(gv, uv, svg_p, svu_p, sud_p, v);
   StorePerm32x8(dst, v, kHadNorm * WhtLaneSign());
+}
+
+// Gate/up role of the decode stage launch, after the workgroup stored its raw sums (plain
+// stores): every wave waits for its stores' acknowledgement, then one thread counts the
+// workgroup in the entry's counter (agent scope).  The last of the entry's stage_arrivals
+// workgroups computes the entry's mid (rows [row0, row0 + nrows), expert e), reading the
+// gate / up sums with the L2 policy (all written on this XCD), writes the down input rows
+// (mid_xd, MFMA row order), waits for their acknowledgement and counts once more.  The same
+// arithmetic as MoeMidKernel (MidBlock), so the rows are bitwise equal.
+__device__ __forceinline__ void StagePublishMid(const GemmArgs& g, int ei, int e, int row0, int nrows) {
+  __shared__ int s_last;
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0)
+    s_last = __hip_atomic_fetch_add(g.stage_ctr + ei * kStageCtrStride, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+             g.stage_arrivals - 1;
+  __syncthreads();
+  if (!s_last) return;
+  const int I = g.ncp * 32, nb = I / 128, j = threadIdx.x & 15;
+  const __amdgpu_buffer_rsrc_t rg = MakeRsrc(g.plane[0].y, 0x7fffffffu), ru = MakeRsrc(g.plane[1].y, 0x7fffffffu);
+  const __half* svg = g.mid_svg + (size_t)e * I;
+  const __half* svu = g.mid_svu + (size_t)e * I;
+  const __half* sud = g.mid_suh + (size_t)e * I;
+  for (int it = (int)threadIdx.x >> 4; it < nrows * nb; it += 16) {  // uniform per 16 lanes
+    const int r = it / nb, blk = it % nb, c0 = blk * 128 + 8 * j;
+    const size_t p = (size_t)(row0 + r);
+    const uint32_t og = (uint32_t)((p * g.plane[0].ldy + c0) * 4), ou = (uint32_t)((p * g.plane[1].ldy + c0) * 4);
+    float gv[8], uv[8];
+    const u32x4_t g0 = BufLoad128L2(rg, og, 0), g1 = BufLoad128L2(rg, og + 16, 0);
+    const u32x4_t u0 = BufLoad128L2(ru, ou, 0), u1 = BufLoad128L2(ru, ou + 16, 0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      gv[i] = __uint_as_float(g0[i]);
+      gv[4 + i] = __uint_as_float(g1[i]);
+      uv[i] = __uint_as_float(u0[i]);
+      uv[4 + i] = __uint_as_float(u1[i]);
+    }
+    MidBlock(gv, uv, svg + c0, svu + c0, sud + c0, g.mid_xd + p * I + blk * 128);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) __hip_atomic_fetch_add(g.stage_ctr + ei * kStageCtrStride, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Wave-uniform load through the scalar cache (device tables written by earlier launches).
@@ -210,7 +262,10 @@ __device__ __forceinline__ MatPtr MatOf(const GemmArgs& g, const GemmPlane& pl, 
 struct NoFill {
   __device__ void operator()() const {}
 };
-template <int K2, int CB, int NRB, int U, bool XL = false, typename Fill = NoFill>
+// XL2: activation loads with the L2 policy (BufLoad128L2: rows published by other
+// workgroups of the same XCD during the launch), and fill() (the wait for them) runs
+// between the first weight loads and the first activation loads.
+template <int K2, int CB, int NRB, int U, bool XL = false, typename Fill = NoFill, bool XL2 = false>
 __device__ __forceinline__ void StreamColumnPair(const uint32_t* tiles, int steps, const __half* x, uint32_t x_bytes,
                                                  const uint32_t (&xrow)[NRB], uint32_t* slot, int lane,
                                                  float4_t (&acc)[NRB][2], const u32x4_t* xl = nullptr,
@@ -240,6 +295,8 @@ __device__ __forceinline__ void StreamColumnPair(const uint32_t* tiles, int step
   auto load_x = [&](int s, int rb) {
     if constexpr (XL)
       return xl[s * 4];
+    else if constexpr (XL2)
+      return BufLoad128L2(rx, xoff[rb], (uint32_t)s * 64);
     else
       return BufLoad128(rx, xoff[rb], (uint32_t)s * 64);
   };
@@ -285,7 +342,7 @@ __device__ __forceinline__ void StreamColumnPair(const uint32_t* tiles, int step
       for (int rb = 0; rb < NRB; ++rb) xg[u][rb] = load_x(sb + u, rb);
     }
   };
-  if constexpr (XL) {
+  if constexpr (XL || XL2) {
 #pragma unroll
     for (int u = 0; u < U; ++u) wa[u] = load_w(u);
     fill();
@@ -319,9 +376,14 @@ __device__ __forceinline__ void StreamColumnPair(const uint32_t* tiles, int step
 // there; rows past the entry read its last row (their sums are discarded).  Each of the
 // entry's column-block workgroups computes the mid again: a few hundred VALU per row
 // block instead of a launch and the down input's round trip through memory.
-template <int K2, int CB, int NRB, int KSW, int U, bool MIDX = false>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NRB == 1 && K2 <= 8 ? 8 : 1)))
-Exl3GemmKernel(GemmArgs g) {
+//
+// STAGE (one role of Exl3DecodeStageKernel, gate/up and down of a decode call in one
+// launch): 1 = gate/up, publishing its sums through the entry's counter and, in the last
+// workgroup of the entry, computing the mid; 2 = down, waiting for the entry's mid rows and
+// reading them with the L2 policy.  (bx, by, bz) are the workgroup's coordinates in the
+// grid of the GEMM's own launch.
+template <int K2, int CB, int NRB, int KSW, int U, bool MIDX, int STAGE>
+__device__ __forceinline__ void GemmBody(const GemmArgs& g, int bx, int by, int bz) {
   static_assert(!MIDX || (NRB == 1 && KSW == 1), "the prologue mid is for the decode down projection");
   constexpr int CPW = 4 / KSW;
   constexpr int T = TileDwords(K2);
@@ -330,12 +392,12 @@ Exl3GemmKernel(GemmArgs g) {
   // Device tables: entries past the last real one have 0 rows (the grid never exceeds the
   // table), so a wave's first weight load waits on two dependent scalar loads (entry,
   // matrix pointers) and no entry count.
-  const int ei = (int)blockIdx.y + g.entry_base;
+  const int ei = by + g.entry_base;
   const int4 ent = EntryOf(g, ei);
   if (g.entries ? ent.z <= 0 : ei >= g.n_entries_host) return;
-  const GemmPlane& pl = g.plane[blockIdx.z];
+  const GemmPlane& pl = g.plane[bz];
   const int ncpg = g.ncp / CPW;
-  const int cpg = blockIdx.x % ncpg, kseg = blockIdx.x / ncpg;
+  const int cpg = bx % ncpg, kseg = bx / ncpg;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int cp = cpg * CPW + wave / KSW, ks = wave % KSW;
   const int nsplit = g.S * KSW, split = kseg * KSW + ks;
@@ -389,6 +451,27 @@ Exl3GemmKernel(GemmArgs g) {
     const int rr = min(lane & 15, nrows - 1);
     StreamColumnPair<K2, CB, NRB, U, true>(m.tiles + ((size_t)cp * g.A + a0) * 2 * T, steps, xb, xbytes, xrow,
                                            stage[wave], lane, acc, xmid + rr * rs + 2 * a0 + (lane >> 4), fill);
+  } else if constexpr (STAGE == 2) {
+    // The entry's mid rows are ready once its counter reaches arrivals + 1.  Bounded: every
+    // gate/up workgroup precedes every down workgroup in dispatch order and never waits, so
+    // the count arrives; the bound only guarantees that every wave exits.
+    // The wait runs after the first weight loads are issued, so their latency overlaps it.
+    __shared__ int s_ready;
+    auto wait = [&]() {
+      if (threadIdx.x == 0) {
+        int it = 0;
+        while (__hip_atomic_load(g.stage_ctr + ei * kStageCtrStride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <
+                   g.stage_arrivals + 1 &&
+               ++it < (1 << 20))
+          __builtin_amdgcn_s_sleep(16);
+        s_ready = it < (1 << 20);
+      }
+      __syncthreads();
+    };
+    StreamColumnPair<K2, CB, NRB, U, false, decltype(wait)&, true>(m.tiles + ((size_t)cp * g.A + a0) * 2 * T, steps,
+                                                                    xb, xbytes, xrow, stage[wave], lane, acc, nullptr,
+                                                                    wait);
+    if (!s_ready) return;  // never taken when the dispatch order holds (the output rows stay unwritten)
   } else {
     StreamColumnPair<K2, CB, NRB, U>(m.tiles + ((size_t)cp * g.A + a0) * 2 * T, steps, xb, xbytes, xrow, stage[wave],
                                      lane, acc);
@@ -406,6 +489,29 @@ Exl3GemmKernel(GemmArgs g) {
       }
     }
     __syncthreads();
+    if constexpr (STAGE == 1) {
+      static_assert(CPW == 1 && NRB == 1, "one storing wave per gate/up workgroup");
+      if (ks == 0) {
+#pragma unroll
+        for (int k = 0; k < KSW - 1; ++k) {
+          acc[0][0] += red[c][k][0][lane];
+          acc[0][1] += red[c][k][1][lane];
+        }
+        float* yr0 = pl.y + (size_t)kseg * pl.seg_stride;
+        const int col = (2 * cp + ((lane & 15) >> 3)) * 16 + (lane & 7);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = 4 * (lane >> 4) + i;
+          if (r < nrows) {
+            float* yr = yr0 + (size_t)(row0 + r) * pl.ldy;
+            yr[col] = acc[0][0][i];
+            yr[col + 8] = acc[0][1][i];
+          }
+        }
+      }
+      StagePublishMid(g, ei, ent.x, row0, nrows);
+      return;
+    }
     if (ks > 0) return;
 #pragma unroll
     for (int k = 0; k < KSW - 1; ++k)
@@ -467,6 +573,36 @@ Exl3GemmKernel(GemmArgs g) {
         yr[col + 8] = acc[rb][1][i];
       }
     }
+}
+
+template <int K2, int CB, int NRB, int KSW, int U, bool MIDX = false>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NRB == 1 && K2 <= 8 ? 8 : 1)))
+Exl3GemmKernel(GemmArgs g) {
+  GemmBody<K2, CB, NRB, KSW, U, MIDX, 0>(g, (int)blockIdx.x, (int)blockIdx.y, (int)blockIdx.z);
+}
+
+// Decode calls: the gate/up GEMM, the mid and the down GEMM (output transform in its
+// epilogue) in one launch, with no fence and no data leaving an XCD.  Workgroups go to the
+// 8 XCDs round-robin by linear id; workgroup L serves row entry e with e % 8 = L % 8, so
+// an entry's gate/up sums and mid rows are written and read in one XCD's L2 (plain stores,
+// acknowledged before an agent-scope counter; reads with the L2 policy).  Ids [0, n_gu):
+// gate/up (per XCD, entry-major: 2 gu.ncp workgroups per entry, column pair then plane);
+// the rest: down (dn.ncp / 4 column-block workgroups per entry).  Every gate/up workgroup
+// precedes every down workgroup in dispatch order, and only down workgroups wait, so every
+// wait ends.  nyp: the entry table's length, a multiple of 8 (entries past the device-side
+// count have 0 rows).  The counters are zeroed by the grouping launch before.
+template <int K2, int CB>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(K2 <= 8 ? 8 : 1)))
+Exl3DecodeStageKernel(GemmArgs gu, GemmArgs dn, int nyp) {
+  const int L = (int)blockIdx.x, x = L & 7;
+  const int per_gu = 2 * gu.ncp, n_gu = per_gu * nyp;
+  if (L < n_gu) {
+    const int k = L >> 3, e = 8 * (k / per_gu) + x, j = k % per_gu;
+    GemmBody<K2, CB, 1, 4, 2, false, 1>(gu, j % gu.ncp, e, j / gu.ncp);
+  } else {
+    const int per_dn = dn.ncp / 4, k = (L - n_gu) >> 3, e = 8 * (k / per_dn) + x, j = k % per_dn;
+    GemmBody<K2, CB, 1, 1, 2, false, 2>(dn, j, e, 0);
+  }
 }
 
 }  // namespace cx

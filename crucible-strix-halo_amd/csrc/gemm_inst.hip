@@ -52,4 +52,20 @@ bool CX_CAT(LaunchGemmRate, CX_RATE)(int cb, int nrb, int ksw, dim3 grid, const 
   return false;
 }
 
+bool CX_CAT(LaunchDecodeStageRate, CX_RATE)(int cb, const GemmArgs& gu, const GemmArgs& dn, int nyp, hipStream_t s) {
+  constexpr int K2 = CX_RATE;
+  const unsigned blocks = (unsigned)((2 * gu.ncp + dn.ncp / 4) * nyp);
+  auto go = [&](auto cbc) {
+    constexpr int CB = decltype(cbc)::value;
+    hipLaunchKernelGGL((Exl3DecodeStageKernel<K2, CB>), dim3(blocks), dim3(256), 0, s, gu, dn, nyp);
+    return true;
+  };
+  if (cb == kCbMul1) return go(IC<kCbMul1>{});
+  if constexpr (K2 % 2 == 0) {
+    if (cb == kCbMcg) return go(IC<kCbMcg>{});
+    if (cb == kCb3Inst) return go(IC<kCb3Inst>{});
+  }
+  return false;
+}
+
 }  // namespace cx

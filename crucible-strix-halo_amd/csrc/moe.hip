@@ -151,6 +151,8 @@ struct GroupOut {
   int chunk;       // rows per entry
   int M, topk, E;
   int max_entries;  // entries [n_entries, max_entries) are written empty (rows = 0)
+  int* zero;        // nzero ints the grouping sets to 0 (the decode stage launch's counters; nullable)
+  int nzero;
 };
 
 // Empty entries after the last real one, so a GEMM launched over max_entries rows of the
@@ -242,6 +244,7 @@ __device__ void WritePair(const GroupOut& o, int p, int i, int e) {
 // in global memory or in LDS.  ref/prefill_ref.py:37-45.
 __device__ void GroupSmallBody(const int* sel, const GroupOut& o, int* s_cur, int* s_scan) {
   const int n = o.M * o.topk;
+  for (int i = threadIdx.x; i < o.nzero; i += blockDim.x) o.zero[i] = 0;
   for (int e = threadIdx.x; e < o.E; e += blockDim.x) s_cur[e] = 0;
   __syncthreads();
   for (int i = threadIdx.x; i < n; i += blockDim.x) {  // counts only; ids outside [0, E) are dropped
@@ -692,7 +695,8 @@ __global__ void __launch_bounds__(256) MoeCombineKernel(const void* __restrict__
 //   CX_DOWN_MID: -1 the decode mid in the down GEMM's prologue at M (topk + 1) <= 128, 0 / 1
 //     never / always (I <= 1024);
 //   CX_FUSED_ROUTE: -1 routing inside the grouping launch at M <= 16, 0 / 1 never / for every
-//     small call.
+//     small call;
+//   CX_STAGE: decode calls with gate/up, mid and down in one launch (0: separate launches).
 struct Switches {
   int nrb, wpg;
   int kernel;
@@ -700,6 +704,7 @@ struct Switches {
   int tall_mid;
   int down_mid;
   int fused_route;
+  int stage;
 };
 inline Switches ReadSwitches() {
   auto env = [](const char* k, int d) {
@@ -709,7 +714,7 @@ inline Switches ReadSwitches() {
   const int nrb = env("CX_PREFILL_NRB", 4) == 8 ? 8 : 4;
   const int w = env("CX_PREFILL_WPG", 4);
   return Switches{nrb, w == 16 && nrb == 4 ? 16 : w == 4 ? 4 : 8, env("CX_PREFILL_GEMM", -1), env("CX_PREFILL_MID", 1),
-                  env("CX_TALL_SEQMID", 1), env("CX_DOWN_MID", -1), env("CX_FUSED_ROUTE", -1)};
+                  env("CX_TALL_SEQMID", 1), env("CX_DOWN_MID", -1), env("CX_FUSED_ROUTE", -1), env("CX_STAGE", 1)};
 }
 
 }  // namespace cx
@@ -733,10 +738,13 @@ namespace cx {
 
 struct MoeSizes {
   int M, P, n, nsh, chunk, nrb, wpg, max_entries, ntiles;
-  bool small, prefill, tall, mid, down_mid, tall_mid;
+  bool small, prefill, tall, mid, down_mid, tall_mid, stage;
   size_t off_sel, off_wts, off_counts, off_offsets, off_pairs, off_rows, off_inv, off_rexp, off_ent, off_nent, off_tiles;
-  size_t off_xg, off_xu, off_yg, off_yu, off_xd, off_yd, off_ysc, total;
+  size_t off_xg, off_xu, off_yg, off_yu, off_xd, off_yd, off_ysc, off_ctr, total;
+  int nyp;  // entry table length of the decode stage launch (max_entries rounded up to 8)
 };
+
+bool FrontEndFits(int M, int E, int topk);
 
 MoeSizes PlanMoe(const cx_moe_plan* pl, int M, int mode) {
   MoeSizes s{};
@@ -765,10 +773,22 @@ MoeSizes PlanMoe(const cx_moe_plan* pl, int M, int mode) {
   // Switch CX_DOWN_MID = 0 / 1 forces it off / on (decode, I <= 1024).
   s.down_mid = decode && pl->I <= 1024 &&
                (ps.down_mid < 0 ? (long)M * (pl->topk + 1) <= 128 : ps.down_mid != 0);
+  // Decode calls through the grouping launch with every matrix at one rate and codebook,
+  // above the prologue mid's range: gate/up, the mid and down in one launch
+  // (Exl3DecodeStageKernel).  Measured on config 3 (median per layer call, 200 calls):
+  // 12 rows 74.8 -> 66.3 us, 16 rows 87.6 -> 80.4, 24 rows 111.7 -> 102.7, 32 rows
+  // 128.8 -> 124, 64 rows 188.7 -> 181; at 1-8 rows, against the down GEMM with the
+  // prologue mid, no change (29.4 / 58.5 us) or a little slower (R = 1 in bench: 31.6
+  // against 30.8 us).
+  s.stage = decode && ps.stage != 0 && FrontEndFits(M, pl->E, pl->topk) && !s.down_mid && pl->k2_gu == pl->k2_d &&
+            pl->k2_gu == pl->k2_sgu && pl->k2_gu == pl->k2_sd && pl->cb_gu == pl->cb_d && pl->cb_gu == pl->cb_sgu &&
+            pl->cb_gu == pl->cb_sd && pl->I % 128 == 0;
   // Decode: one 16-row block per entry; prefill: every row of an entry shares each decoded tile.
   s.chunk = 16 * s.nrb;
   s.nsh = (M + s.chunk - 1) / s.chunk;
   s.max_entries = s.nsh + std::min(pl->E, s.n) + s.n / s.chunk;
+  s.nyp = (s.max_entries + 7) / 8 * 8;
+  if (s.stage) s.max_entries = s.nyp;  // the stage launch's XCD mapping reads whole groups of 8
   s.small = s.n <= kSmallRoutes;
   s.ntiles = (s.n + kTile - 1) / kTile;
   size_t o = 0;
@@ -795,6 +815,7 @@ MoeSizes PlanMoe(const cx_moe_plan* pl, int M, int mode) {
   s.off_xd = take((size_t)s.P * pl->I * 2);
   s.off_yd = take((size_t)s.P * pl->H * (s.prefill ? 2 : 4));
   s.off_ysc = take(s.prefill ? (size_t)s.P * (pl->H / 128) * 4 : 0);
+  s.off_ctr = take(s.stage ? (size_t)s.nyp * kStageCtrStride * 4 : 0);
   s.total = o;
   return s;
 }
@@ -859,9 +880,9 @@ int LaunchGroup(const int* sel, GroupOut& o, int* tile_counts, int ntiles, hipSt
 // Expert GEMM over the device-built entries: shared-expert entries [0, nsh) and routed
 // entries [nsh, n_entries).  Routed and shared matrices with different rates go in
 // separate launches.
-bool LaunchExpertGemm(const cx_moe_plan* pl, const MoeSizes& sz, bool gate_up, const __half* xa, const __half* xb,
-                      float* ya, float* yb, float* ysc, __half* xd, const int4* ent, const int* nent, const int* xmap,
-                      const float* mid_yg, const float* mid_yu, hipStream_t s) {
+GemmArgs ExpertGemmArgs(const cx_moe_plan* pl, const MoeSizes& sz, bool gate_up, const __half* xa, const __half* xb,
+                        float* ya, float* yb, float* ysc, __half* xd, const int4* ent, const int* xmap,
+                        const float* mid_yg, const float* mid_yu) {
   GemmArgs g{};
   if (mid_yg) {
     g.mid_yg = mid_yg;
@@ -889,9 +910,16 @@ bool LaunchExpertGemm(const cx_moe_plan* pl, const MoeSizes& sz, bool gate_up, c
                             : GemmPlane{pl->tb.down, xa, ya, in, out, 0, 1, nullptr};
     g.plane[1] = g.plane[0];
   }
+  g.tall_seq_mid = gate_up && sz.tall_mid;
+  return g;
+}
+
+bool LaunchExpertGemm(const cx_moe_plan* pl, const MoeSizes& sz, bool gate_up, const __half* xa, const __half* xb,
+                      float* ya, float* yb, float* ysc, __half* xd, const int4* ent, const int* nent, const int* xmap,
+                      const float* mid_yg, const float* mid_yu, hipStream_t s) {
+  GemmArgs g = ExpertGemmArgs(pl, sz, gate_up, xa, xb, ya, yb, ysc, xd, ent, xmap, mid_yg, mid_yu);
   const int ksw = gate_up ? 4 : 1;
   const int planes = gate_up && !sz.tall_mid ? 2 : 1;
-  g.tall_seq_mid = gate_up && sz.tall_mid;
   const int k2r = gate_up ? pl->k2_gu : pl->k2_d, cbr = gate_up ? pl->cb_gu : pl->cb_d;
   const int k2s = gate_up ? pl->k2_sgu : pl->k2_sd, cbs = gate_up ? pl->cb_sgu : pl->cb_sd;
   const int wpg = g.ncp % sz.wpg == 0 ? sz.wpg : 4;
@@ -1119,7 +1147,9 @@ int MoeForward(const cx_moe_plan* pl, const void* x, int32_t x_dtype, int32_t ld
     }
   };
   mark();
-  GroupOut o{counts, offsets, pairs, rows, inv, rexp, ent, nent, sz.chunk, M, pl->topk, pl->E, sz.max_entries};
+  int* ctr = reinterpret_cast<int*>(ws + sz.off_ctr);
+  GroupOut o{counts, offsets, pairs, rows, inv, rexp, ent, nent, sz.chunk, M, pl->topk, pl->E, sz.max_entries,
+             sz.stage ? ctr : nullptr, sz.stage ? sz.nyp * kStageCtrStride : 0};
   const bool front = !sz.prefill && FrontEndFits(M, pl->E, pl->topk);
   // Routing fused into the grouping launch when workgroup 0 routes every row in one round
   // of its 16 waves (M <= 16; CX_FUSED_ROUTE = 0 / 1 forces it off / on for any small call).
@@ -1162,17 +1192,33 @@ int MoeForward(const cx_moe_plan* pl, const void* x, int32_t x_dtype, int32_t ld
                          pl->topk, pl->E, pl->H, S, xg, xu);
   }
   mark();
-  if (!LaunchExpertGemm(pl, sz, true, xg, xu, yg, yu, nullptr, xd, ent, nent, front ? pairs : nullptr, nullptr, nullptr,
-                        s))
-    return CX_E_UNSUPPORTED;
-  mark();
-  if (!sz.mid && !sz.down_mid && !sz.tall_mid)  // else a GEMM computes the down projection's input rows itself
-    hipLaunchKernelGGL(MoeMidKernel, dim3((unsigned)((sz.P + 3) / 4)), dim3(256), 0, s, yg, yu, rexp,
-                       pl->tb, M, pl->topk, pl->E, pl->I, xd);
-  mark();
-  if (!LaunchExpertGemm(pl, sz, false, xd, nullptr, yd, nullptr, ysc, nullptr, ent, nent, nullptr,
-                        sz.down_mid ? yg : nullptr, sz.down_mid ? yu : nullptr, s))
-    return CX_E_UNSUPPORTED;
+  if (sz.stage) {
+    // Gate/up, mid and down in one launch (the counters were zeroed by the grouping launch);
+    // the trace records it as the gate/up stage (mid and down stages empty).
+    GemmArgs gu = ExpertGemmArgs(pl, sz, true, xg, xu, yg, yu, nullptr, xd, ent, pairs, nullptr, nullptr);
+    GemmArgs dn = ExpertGemmArgs(pl, sz, false, xd, nullptr, yd, nullptr, nullptr, nullptr, ent, nullptr, nullptr,
+                                 nullptr);
+    gu.mid_svg = pl->tb.gate_svh;
+    gu.mid_svu = pl->tb.up_svh;
+    gu.n_entries = dn.n_entries = nent;
+    gu.stage_ctr = dn.stage_ctr = ctr;
+    gu.stage_arrivals = dn.stage_arrivals = 2 * gu.ncp;
+    if (!LaunchDecodeStage(pl->k2_gu, pl->cb_gu, gu, dn, sz.nyp, s)) return CX_E_UNSUPPORTED;
+    mark();
+    mark();
+  } else {
+    if (!LaunchExpertGemm(pl, sz, true, xg, xu, yg, yu, nullptr, xd, ent, nent, front ? pairs : nullptr, nullptr,
+                          nullptr, s))
+      return CX_E_UNSUPPORTED;
+    mark();
+    if (!sz.mid && !sz.down_mid && !sz.tall_mid)  // else a GEMM computes the down projection's input rows itself
+      hipLaunchKernelGGL(MoeMidKernel, dim3((unsigned)((sz.P + 3) / 4)), dim3(256), 0, s, yg, yu, rexp,
+                         pl->tb, M, pl->topk, pl->E, pl->I, xd);
+    mark();
+    if (!LaunchExpertGemm(pl, sz, false, xd, nullptr, yd, nullptr, ysc, nullptr, ent, nent, nullptr,
+                          sz.down_mid ? yg : nullptr, sz.down_mid ? yu : nullptr, s))
+      return CX_E_UNSUPPORTED;
+  }
   mark();
   {
     const long items = (long)M * (pl->H / (sz.prefill ? 8 : 4));  // columns per thread: MoeCombineKernel's CW
