@@ -25,7 +25,9 @@ def test_graph_replays_match_eager(synth):
     lin = synth.device_linear(gen, 512, 1024, 4)
     rng = np.random.default_rng(8)
     cases = []
-    for mode, M in ((CX_MOE_DECODE, 13), (CX_MOE_PREFILL, 300)):
+    # decode at 13 rows (the mid in the down GEMM's prologue) and at 20 rows (gate/up, mid and
+    # down in one stage launch, counters zeroed by the grouping launch), and prefill
+    for mode, M in ((CX_MOE_DECODE, 13), (CX_MOE_DECODE, 20), (CX_MOE_PREFILL, 300)):
         x = torch.from_numpy(rng.standard_normal((M, 512)).astype(np.float16)).cuda()
         lg = torch.from_numpy(rng.standard_normal((M, 65)).astype(np.float32)).cuda()
         ws = torch.empty(plan.workspace_size(M, mode), dtype=torch.uint8, device="cuda")
