@@ -11,7 +11,7 @@ import os
 from pathlib import Path
 
 PKG_DIR = Path(__file__).resolve().parent.parent
-LIB_PATH = Path(os.environ.get("CX_LIB", PKG_DIR / "libcrucible_exl3.so"))
+LIB_PATH = Path(os.environ.get("CX_LIB") or (PKG_DIR / "libcrucible_exl3.so"))
 
 CX_CB = {"3inst": 0, "mcg": 1, "mul1": 2}
 CX_F16, CX_F32 = 0, 1
