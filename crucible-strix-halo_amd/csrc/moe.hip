@@ -151,8 +151,8 @@ struct GroupOut {
   int chunk;       // rows per entry
   int M, topk, E;
   int max_entries;  // entries [n_entries, max_entries) are written empty (rows = 0)
-  int* zero;        // nzero ints the grouping sets to 0 (the decode stage launch's counters; nullable)
-  int nzero;
+  int* zero;        // the decode stage launch's nzero counters, zero[i * kStageCtrStride], which the
+  int nzero;        // grouping sets to 0 (nullable)
 };
 
 // Empty entries after the last real one, so a GEMM launched over max_entries rows of the
@@ -244,7 +244,7 @@ __device__ void WritePair(const GroupOut& o, int p, int i, int e) {
 // in global memory or in LDS.  ref/prefill_ref.py:37-45.
 __device__ void GroupSmallBody(const int* sel, const GroupOut& o, int* s_cur, int* s_scan) {
   const int n = o.M * o.topk;
-  for (int i = threadIdx.x; i < o.nzero; i += blockDim.x) o.zero[i] = 0;
+  for (int i = threadIdx.x; i < o.nzero; i += blockDim.x) o.zero[i * kStageCtrStride] = 0;
   for (int e = threadIdx.x; e < o.E; e += blockDim.x) s_cur[e] = 0;
   __syncthreads();
   for (int i = threadIdx.x; i < n; i += blockDim.x) {  // counts only; ids outside [0, E) are dropped
@@ -1149,7 +1149,7 @@ int MoeForward(const cx_moe_plan* pl, const void* x, int32_t x_dtype, int32_t ld
   mark();
   int* ctr = reinterpret_cast<int*>(ws + sz.off_ctr);
   GroupOut o{counts, offsets, pairs, rows, inv, rexp, ent, nent, sz.chunk, M, pl->topk, pl->E, sz.max_entries,
-             sz.stage ? ctr : nullptr, sz.stage ? sz.nyp * kStageCtrStride : 0};
+             sz.stage ? ctr : nullptr, sz.stage ? sz.nyp : 0};
   const bool front = !sz.prefill && FrontEndFits(M, pl->E, pl->topk);
   // Routing fused into the grouping launch when workgroup 0 routes every row in one round
   // of its 16 waves (M <= 16; CX_FUSED_ROUTE = 0 / 1 forces it off / on for any small call).
