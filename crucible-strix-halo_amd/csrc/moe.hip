@@ -731,6 +731,7 @@ struct cx_moe_plan {
   hipEvent_t* trace;                 // caller's events (nullable), recorded between stages
   int n_trace, trace_cursor;
   void* scratch;                     // this device's address of the library's static scratch (nullable)
+  bool xcd_rr;                       // workgroups go to the XCDs round-robin (XcdRoundRobin)
   cx::Switches sw;                   // environment switches, read when the plan is created
 };
 
@@ -780,7 +781,7 @@ MoeSizes PlanMoe(const cx_moe_plan* pl, int M, int mode) {
   // 128.8 -> 124, 64 rows 188.7 -> 181; at 1-8 rows, against the down GEMM with the
   // prologue mid, no change (29.4 / 58.5 us) or a little slower (R = 1 in bench: 31.6
   // against 30.8 us).
-  s.stage = decode && ps.stage != 0 && FrontEndFits(M, pl->E, pl->topk) && !s.down_mid && pl->k2_gu == pl->k2_d &&
+  s.stage = decode && ps.stage != 0 && pl->xcd_rr && FrontEndFits(M, pl->E, pl->topk) && !s.down_mid && pl->k2_gu == pl->k2_d &&
             pl->k2_gu == pl->k2_sgu && pl->k2_gu == pl->k2_sd && pl->cb_gu == pl->cb_d && pl->cb_gu == pl->cb_sgu &&
             pl->cb_gu == pl->cb_sd && pl->I % 128 == 0;
   // Decode: one 16-row block per entry; prefill: every row of an entry shares each decoded tile.
@@ -848,6 +849,40 @@ void* StaticScratch(hipError_t* err) {
     g_scratch[dev] = p;
   }
   return g_scratch[dev];
+}
+
+// The decode stage launch (Exl3DecodeStageKernel) keeps each row entry on one XCD by
+// relying on workgroups going to the XCDs round-robin by linear id (ids equal modulo 8 on
+// one XCD; also true of partition modes with 4, 2 or 1 XCDs).  Checked once per device: a
+// probe launch records the XCC id of each of 256 workgroups.
+__global__ void __launch_bounds__(64) XccProbeKernel(int* out) {
+  if (threadIdx.x == 0) {
+    uint32_t v;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+    out[blockIdx.x] = (int)(v & 0xf);
+  }
+}
+int g_xcd_rr[kMaxDevices];  // 0 not probed yet, 1 round-robin, -1 not (or the probe failed)
+
+bool XcdRoundRobin() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return false;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_xcd_rr[dev] == 0) {
+    constexpr int kN = 256;
+    int* d = nullptr;
+    int h[kN];
+    bool ok = hipMalloc(&d, kN * sizeof(int)) == hipSuccess;
+    if (ok) {
+      hipLaunchKernelGGL(XccProbeKernel, dim3(kN), dim3(64), 0, nullptr, d);
+      ok = hipGetLastError() == hipSuccess && hipMemcpy(h, d, sizeof h, hipMemcpyDeviceToHost) == hipSuccess;
+    }
+    if (d) (void)hipFree(d);
+    for (int i = 8; ok && i < kN; ++i) ok = h[i] == h[i % 8];
+    (void)hipGetLastError();
+    g_xcd_rr[dev] = ok ? 1 : -1;
+  }
+  return g_xcd_rr[dev] > 0;
 }
 
 void LaunchRoute(const float* logits, int ld, int M, int E, int topk, const float* shared_logit, int* sel, float* wts,
@@ -1075,6 +1110,7 @@ int cx_moe_plan_create(const cx_moe_layer* layer, cx_moe_plan** out) {
   pl->tb = ExpertTables{pl->d_tables, pl->d_tables + n, pl->d_tables + 2 * n, g_suh, u_suh, g_svh, u_svh, d_suh};
   // The static scratch serves only cx_moe_layer_forward_static: a failed lookup leaves it
   // null (that entry point then returns CX_E_ARG) and does not fail the plan.
+  pl->xcd_rr = XcdRoundRobin();
   pl->scratch = StaticScratch(&err);
   if (err != hipSuccess) {
     pl->scratch = nullptr;
