@@ -192,6 +192,30 @@ def test_smallest_shapes(ops):
         assert e <= 1e-3
 
 
+@pytest.mark.parametrize("E,H,Ie,k", [(32, 1024, 1536, 4), (24, 1536, 640, 3)])
+def test_uneven_block_counts(ops, E, H, Ie, k):
+    # Widths with odd numbers of 128-blocks and column pairs that are not powers of two
+    # (I = 1536: 48 gate/up column pairs, above the prologue mid's I <= 1024; I = 640: 5
+    # Hadamard blocks; H = 1536: 12 down column blocks): decode with the prologue mid (where
+    # it applies), the stage launch and the separate launches, the register-blocked and the
+    # tall prefill, every row against the oracle.
+    from exl3moe import synth
+    plan = synth.device_moe_layer(61 + E, E=E, H=H, Ie=Ie, topk=k)
+    rng = np.random.default_rng(E + H)
+    for M, mode in ((1, 1), (6, 1), (40, 1), (200, 2), (1200, 2)):
+        x = rng.standard_normal((M, H)).astype(np.float16)
+        lg = rng.standard_normal((M, E + 1)).astype(np.float32)
+        print(f"uneven E={E} H={H} I={Ie} k={k} M={M} mode={mode}", flush=True)
+        y, sel, wts = run_layer(plan, x, lg, mode)
+        rs, rw = O.route(lg, E, k)
+        np.testing.assert_array_equal(sel, rs)
+        ref = oracle_layer(plan, x, rs, rw)
+        e = rel_l2(y, ref)
+        print(f"  rel_l2={e:.3e}")
+        assert e <= 1e-3
+        assert np.abs(y - ref).max() <= 2e-3 * np.abs(ref).max()
+
+
 def test_tall_prefill_mixed_rates(ops):
     # The shared expert at other rates than the routed ones: each GEMM runs as two launches
     # (shared entries, then routed), and the tall gate/up launch computes the mid itself in
