@@ -147,6 +147,32 @@ def test_rows_invariant_to_batch(ops):
         np.testing.assert_array_equal(part.view(np.uint32), full[:M].view(np.uint32))
 
 
+@pytest.mark.parametrize("I,Ot", [(640, 1536), (1536, 640), (384, 2176)])
+def test_linear_uneven_widths(ops, I, Ot):
+    # Odd numbers of 128-blocks on either side (K splits of unequal step counts, output
+    # column blocks not a power of two): decode and prefill row counts against the oracle,
+    # and rows bitwise invariant to the batch.
+    from exl3moe import synth
+    rng = np.random.default_rng(I + Ot)
+    tr, suh, svh = synth.linear(rng, I, Ot, 4)
+    lin = ops.DeviceLinear.from_trellis(tr, suh, svh, 4)
+    w = O.reconstruct_inner(tr, 4)
+    x = rng.standard_normal((300, I)).astype(np.float16)
+    xd = torch.from_numpy(x).cuda()
+    full = None
+    for M in (1, 24, 300):
+        y = lin(xd[:M].contiguous(), torch.float32).cpu().numpy()
+        ref = O.matvec(x[:M], w, suh, svh, np.float32)
+        print(f"linear {I}->{Ot} M={M} rel_l2={rel_l2(y, ref):.3e}")
+        assert rel_l2(y, ref) <= 1e-3
+        assert np.abs(y - ref).max() <= 1e-3 * np.abs(ref).max()
+        if M == 24:
+            full = y
+        elif M == 1:
+            first = y
+    np.testing.assert_array_equal(first.view(np.uint32), full[:1].view(np.uint32))
+
+
 def test_linear_large_m_prefill_rows(ops):
     from exl3moe import synth
     rng = np.random.default_rng(8)
