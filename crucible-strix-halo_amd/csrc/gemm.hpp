@@ -585,22 +585,27 @@ Exl3GemmKernel(GemmArgs g) {
 // epilogue) in one launch, with no fence and no data leaving an XCD.  Workgroups go to the
 // 8 XCDs round-robin by linear id; workgroup L serves row entry e with e % 8 = L % 8, so
 // an entry's gate/up sums and mid rows are written and read in one XCD's L2 (plain stores,
-// acknowledged before an agent-scope counter; reads with the L2 policy).  Ids [0, n_gu):
-// gate/up (per XCD, entry-major: 2 gu.ncp workgroups per entry, column pair then plane);
-// the rest: down (dn.ncp / 4 column-block workgroups per entry).  Every gate/up workgroup
-// precedes every down workgroup in dispatch order, and only down workgroups wait, so every
-// wait ends.  nyp: the entry table's length, a multiple of 8 (entries past the device-side
-// count have 0 rows).  The counters are zeroed by the grouping launch before.
+// acknowledged before an agent-scope counter; reads with the L2 policy).  With n the
+// device-side entry count rounded up to 8: ids [0, n_gu = 2 gu.ncp n): gate/up (per XCD,
+// entry-major: 2 gu.ncp workgroups per entry, column pair then plane); the next dn.ncp / 4
+// n ids: down (column-block workgroups per entry); the rest (the grid is sized for the
+// table's nyp entries) exit at once, after every real workgroup in dispatch order, so the
+// dispatcher's time on them falls in the launch's drain instead of between the gate/up and
+// the down workgroups.  Every gate/up workgroup precedes every down workgroup in dispatch
+// order, and only down workgroups wait, so every wait ends.  nyp: the entry table's
+// length, a multiple of 8 (entries past the device-side count have 0 rows).  The counters
+// are zeroed by the grouping launch before.
 template <int K2, int CB>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(K2 <= 8 ? 8 : 1)))
 Exl3DecodeStageKernel(GemmArgs gu, GemmArgs dn, int nyp) {
   const int L = (int)blockIdx.x, x = L & 7;
-  const int per_gu = 2 * gu.ncp, n_gu = per_gu * nyp;
+  const int n = (min(*gu.n_entries, nyp) + 7) & ~7;
+  const int per_gu = 2 * gu.ncp, n_gu = per_gu * n, per_dn = dn.ncp / 4;
   if (L < n_gu) {
     const int k = L >> 3, e = 8 * (k / per_gu) + x, j = k % per_gu;
     GemmBody<K2, CB, 1, 4, 2, false, 1>(gu, j % gu.ncp, e, j / gu.ncp);
-  } else {
-    const int per_dn = dn.ncp / 4, k = (L - n_gu) >> 3, e = 8 * (k / per_dn) + x, j = k % per_dn;
+  } else if (L < n_gu + per_dn * n) {
+    const int k = (L - n_gu) >> 3, e = 8 * (k / per_dn) + x, j = k % per_dn;
     GemmBody<K2, CB, 1, 1, 2, false, 2>(dn, j, e, 0);
   }
 }
