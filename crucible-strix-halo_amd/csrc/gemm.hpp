@@ -535,6 +535,10 @@ __device__ __forceinline__ void GemmBody(const GemmArgs& g, int bx, int by, int 
         __shared__ float ebuf_s[16 * NRB][132];
         ebuf = ebuf_s;
       }
+      // The output scales are loaded first: their latency overlaps the staging.
+      const int j = threadIdx.x & 15, c0 = cpg * 128 + 8 * j;
+      float sv[8];
+      LoadH8(m.svh + c0, sv);
       const int cl = wave * 32 + ((lane & 15) >> 3) * 16 + (lane & 7);
 #pragma unroll
       for (int rb = 0; rb < NRB; ++rb)
@@ -545,9 +549,6 @@ __device__ __forceinline__ void GemmBody(const GemmArgs& g, int bx, int by, int 
           ebuf[r][cl + 8] = acc[rb][1][i];
         }
       __syncthreads();
-      const int j = threadIdx.x & 15, c0 = cpg * 128 + 8 * j;
-      float sv[8];
-      LoadH8(m.svh + c0, sv);
       for (int r = threadIdx.x >> 4; r < nrows; r += 16) {
         float v[8];
 #pragma unroll
