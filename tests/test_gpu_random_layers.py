@@ -1,8 +1,8 @@
 """MoE layers of seeded random shapes, rates, codebooks and row counts against the oracle.
 
 Each case draws E (2-96 experts), top-k (1-min(E, 16)), hidden and expert widths (128-1024
-in 128 steps), the routed experts' gate/up and down rates, the shared expert's rates (the
-same or different), the codebook, the row count (1-400, ragged sessions some of the time)
+in 128 steps), the codebook, the routed experts' gate/up and down rates (2-8 bits per
+weight, and 1.5 / 2.5 / 3.5 for mul1), the shared expert's rates (the same or different), the row count (1-400, ragged sessions some of the time)
 and the mode (decode, prefill, auto) from a fixed seed, so the kernels' less common
 combinations (mixed rates, which take separate shared and routed launches; few experts,
 which leave XCDs without entries; short last row blocks) run against the oracle: routing
@@ -16,7 +16,8 @@ from test_gpu_moe import oracle_layer, rel_l2
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
 
-RATES = (2, 3, 4, 5, 6)  # bits per weight: the rates every codebook supports
+RATES = (2, 3, 4, 5, 6, 7, 8)  # bits per weight: the rates every codebook supports
+HALF_RATES = (1.5, 2.5, 3.5)  # mul1 only
 
 
 def _case(seed):
@@ -25,17 +26,18 @@ def _case(seed):
     k = int(rng.integers(1, min(E, 16) + 1))
     H = 128 * int(rng.integers(1, 9))
     Ie = 128 * int(rng.integers(1, 9))
-    bgu, bd = (int(b) for b in rng.choice(RATES, 2))
-    mixed = rng.random() < 0.3
-    sgu, sd = (int(b) for b in rng.choice(RATES, 2)) if mixed else (bgu, bd)
     cb = str(rng.choice(["mul1", "mul1", "mcg", "3inst"]))
+    rates = RATES + HALF_RATES if cb == "mul1" else RATES
+    bgu, bd = (float(b) for b in rng.choice(rates, 2))
+    mixed = rng.random() < 0.3
+    sgu, sd = (float(b) for b in rng.choice(rates, 2)) if mixed else (bgu, bd)
     M = int(rng.integers(1, 401)) if rng.random() < 0.5 else int(rng.integers(1, 41))
     mode = int(rng.choice([0, 1, 2]))  # auto, decode, prefill
     ragged = rng.random() < 0.3
     return dict(E=E, k=k, H=H, Ie=Ie, bgu=bgu, bd=bd, sgu=sgu, sd=sd, cb=cb, M=M, mode=mode, ragged=ragged)
 
 
-@pytest.mark.parametrize("seed", range(24))
+@pytest.mark.parametrize("seed", range(48))
 def test_random_layer(seed):
     if not torch.cuda.is_available():
         pytest.skip("no GPU")
