@@ -317,3 +317,40 @@ def test_output_transform_bit_exact(ops):
     yh = y.astype(np.float16).astype(np.float32)
     want = (O.hadamard(yh).astype(np.float16).astype(np.float32) * svh.astype(np.float32)).astype(np.float16)
     _same_values(got, want)
+
+
+@pytest.mark.parametrize("seed", range(32))
+def test_random_linear(ops, seed):
+    # Seeded random widths (128-2048 in 128 steps on either side), rate, codebook, row
+    # count (1-300, ragged sessions some of the time), input and output dtypes, and a
+    # strided input: outputs against the oracle, and fp32 inputs bitwise equal to the same
+    # values rounded to fp16 first.
+    from exl3moe import synth
+    rng = np.random.default_rng(5000 + seed)
+    I, Ot = 128 * int(rng.integers(1, 17)), 128 * int(rng.integers(1, 17))
+    cb = str(rng.choice(["mul1", "mul1", "mcg", "3inst"]))
+    bits = float(rng.choice(RATES if cb == "mul1" else [2, 3, 4, 5, 6, 7, 8]))
+    M = int(rng.integers(1, 301)) if rng.random() < 0.5 else int(rng.integers(1, 41))
+    f32_in, f16_out = bool(rng.random() < 0.4), bool(rng.random() < 0.4)
+    offs = None
+    if M >= 2 and rng.random() < 0.3:
+        cuts = np.sort(rng.choice(np.arange(1, M), size=min(7, M - 1), replace=False))
+        offs = [0] + cuts.tolist() + [M]
+    print(f"random linear seed={seed} {I}->{Ot} bits={bits} cb={cb} M={M} f32_in={f32_in} f16_out={f16_out} "
+          f"ragged={offs is not None}", flush=True)
+    tr, suh, svh = synth.linear(rng, I, Ot, bits)
+    lin = ops.DeviceLinear.from_trellis(tr, suh, svh, bits, codebook=cb)
+    xf = rng.standard_normal((M, I + 32)).astype(np.float32)
+    xh = xf[:, :I].astype(np.float16)
+    x = torch.from_numpy(xf if f32_in else xf.astype(np.float16)).cuda()[:, :I]  # strided rows
+    ydt = torch.float16 if f16_out else torch.float32
+    y = lin(x, ydt, row_offsets=offs).cpu().numpy()
+    if f32_in:
+        y16 = lin(torch.from_numpy(np.ascontiguousarray(xh)).cuda(), ydt, row_offsets=offs).cpu().numpy()
+        np.testing.assert_array_equal(y.view(np.uint16 if f16_out else np.uint32),
+                                      y16.view(np.uint16 if f16_out else np.uint32))
+    ref = O.matvec(xh, O.reconstruct_inner(tr, bits, cb), suh, svh, np.float16 if f16_out else np.float32)
+    e = rel_l2(y, ref)
+    print(f"  rel_l2={e:.3e}")
+    assert e <= 1e-3
+    assert np.abs(y.astype(np.float64) - ref).max() <= 1e-3 * np.abs(ref).max() + (2e-3 if f16_out else 0)
