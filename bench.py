@@ -334,7 +334,41 @@ def bench_linear(seed, copies=128, warmup=10):
         out[f"{I}x{O}"] = {"us": pct(ms[:, j] * 1000), "algorithmic_GBps": round(gbs, 1),
                            "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
                            "rows_per_s": round(float(Ms.sum() / (ms[:, j].sum() / 1000)), 1)}
-    del pairs
+    # A group of linears over the same rows (cx_exl3_group, e.g. the q / k / v projections):
+    # 2048 -> 4096 (the pairs' first matrices), 512 and 512, at 4 bpw; the three GEMMs of
+    # one rate run as one launch.
+    from exl3moe import ops
+    kv = [(synth.device_linear(gen, 2048, 512, 4), synth.device_linear(gen, 2048, 512, 4)) for _ in range(copies)]
+    for a, b in kv:
+        a.trellis = b.trellis = None
+    yk = torch.empty(40, 512, dtype=torch.float32, device="cuda")
+    yv = torch.empty(40, 512, dtype=torch.float32, device="cuda")
+    gws = torch.empty(int(ops.group_workspace_size([pairs[0][0], kv[0][0], kv[0][1]], 40)), dtype=torch.uint8,
+                      device="cuda")
+
+    def gcall(i):
+        offs, x1, _ = batches[i % len(batches)]
+        M = offs[-1]
+        ops.linear_group([(pairs[i % copies][0], x1, y1[:M]), (kv[i % copies][0], x1, yk[:M]),
+                          (kv[i % copies][1], x1, yv[:M])], row_offsets=offs, workspace=gws)
+
+    for i in range(warmup):
+        gcall(i)
+    torch.cuda.synchronize()
+    t = EventTimer(copies, torch.cuda.current_stream().cuda_stream)
+    for i in range(copies):
+        t.mark()
+        gcall(warmup + i)
+    t.mark()
+    gms = np.array(t.ms())
+    t.close()
+    Ms = np.array([batches[(warmup + i) % len(batches)][0][-1] for i in range(copies)])
+    by = sum(matrix_bytes(2048, O, 8) + Ms * 2048 * 2 + Ms * O * 4 for O in (4096, 512, 512))
+    gbs = float(by.sum() / (gms.sum() / 1000)) / 1e9
+    out["group_qkv"] = {"workload": "cx_exl3_group of 2048->4096, 2048->512, 2048->512 at 4 bpw over the same rows",
+                        "us": pct(gms * 1000), "algorithmic_GBps": round(gbs, 1),
+                        "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+    del pairs, kv
     torch.cuda.empty_cache()
     return out
 

@@ -225,6 +225,23 @@ bool LaunchDecodeStage(int k2, int cb, const GemmArgs& gu, const GemmArgs& dn, i
   }
 }
 
+bool LaunchGemmMulti(int k2, int cb, int nrb, const GemmMulti& gm, hipStream_t s) {
+  switch (k2) {
+    case 2: return LaunchGemmMultiRate2(cb, nrb, gm, s);
+    case 3: return LaunchGemmMultiRate3(cb, nrb, gm, s);
+    case 4: return LaunchGemmMultiRate4(cb, nrb, gm, s);
+    case 5: return LaunchGemmMultiRate5(cb, nrb, gm, s);
+    case 6: return LaunchGemmMultiRate6(cb, nrb, gm, s);
+    case 7: return LaunchGemmMultiRate7(cb, nrb, gm, s);
+    case 8: return LaunchGemmMultiRate8(cb, nrb, gm, s);
+    case 10: return LaunchGemmMultiRate10(cb, nrb, gm, s);
+    case 12: return LaunchGemmMultiRate12(cb, nrb, gm, s);
+    case 14: return LaunchGemmMultiRate14(cb, nrb, gm, s);
+    case 16: return LaunchGemmMultiRate16(cb, nrb, gm, s);
+    default: return false;
+  }
+}
+
 bool LaunchGemmTall(int k2, int cb, dim3 grid, const GemmArgs& g, hipStream_t s) {
   switch (k2) {
     case 2: return LaunchGemmTallRate2(cb, grid, g, s);
@@ -246,9 +263,10 @@ size_t LinearWorkspace(const LinearPlan& p, int I, int O, int M) {
   return AlignUp((size_t)M * I * 2, 256) + AlignUp((size_t)p.S * M * O * 4, 256);
 }
 
-// One group of linears over the same M rows: the grouped input transform, one GEMM
-// launch per job (dense row entries, no device tables), the grouped output transform.
-// Jobs are checked by the caller; ws holds each job's transformed input and partials.
+// One group of linears over the same M rows: the grouped input transform, the GEMMs (dense
+// row entries, no device tables; the jobs of one rate and codebook in one launch, up to
+// kMaxMultiJobs a launch), the grouped output transform.  Jobs are checked by the caller;
+// ws holds each job's transformed input and partials.
 int RunGroup(const cx_exl3_job* jobs, int n, int M, char* ws, hipStream_t s) {
   XfInTable tin{};
   XfOutTable tout{};
@@ -287,10 +305,28 @@ int RunGroup(const cx_exl3_job* jobs, int n, int M, char* ws, hipStream_t s) {
     ps[j] = p;
   }
   hipLaunchKernelGGL(InputTransformKernel, dim3((unsigned)((in_items * 16 + 255) / 256)), dim3(256), 0, s, tin);
+  // Every job has the same row count, so the same row-block count, and the same in-workgroup
+  // K split (4): jobs of one rate and codebook can share a launch.
+  std::vector<bool> done(n, false);
   for (int j = 0; j < n; ++j) {
-    const LinearPlan& p = ps[j];
-    const dim3 grid(p.ncp / (4 / p.ksw) * p.S, p.n_entries, 1);
-    if (!LaunchGemm(jobs[j].m.k2, jobs[j].m.codebook, p.nrb, p.ksw, p.u, grid, gs[j], s)) return CX_E_UNSUPPORTED;
+    if (done[j]) continue;
+    GemmMulti gm{};
+    for (int i = j; i < n && gm.n < kMaxMultiJobs; ++i) {
+      if (done[i] || jobs[i].m.k2 != jobs[j].m.k2 || jobs[i].m.codebook != jobs[j].m.codebook) continue;
+      const LinearPlan& p = ps[i];
+      gm.gx[gm.n] = p.ncp / (4 / p.ksw) * p.S;
+      gm.g[gm.n] = gs[i];
+      gm.start[gm.n + 1] = gm.start[gm.n] + gm.gx[gm.n] * p.n_entries;
+      ++gm.n;
+      done[i] = true;
+    }
+    if (gm.n == 1) {
+      const LinearPlan& p = ps[j];
+      const dim3 grid(p.ncp / (4 / p.ksw) * p.S, p.n_entries, 1);
+      if (!LaunchGemm(jobs[j].m.k2, jobs[j].m.codebook, p.nrb, p.ksw, p.u, grid, gs[j], s)) return CX_E_UNSUPPORTED;
+    } else if (!LaunchGemmMulti(jobs[j].m.k2, jobs[j].m.codebook, ps[j].nrb, gm, s)) {
+      return CX_E_UNSUPPORTED;
+    }
   }
   hipLaunchKernelGGL(OutputTransformKernel, dim3((unsigned)((out_items * 16 + 255) / 256)), dim3(256), 0, s, tout);
   return LaunchStatus();

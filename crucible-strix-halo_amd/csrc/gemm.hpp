@@ -582,6 +582,28 @@ Exl3GemmKernel(GemmArgs g) {
   GemmBody<K2, CB, NRB, KSW, U, MIDX, 0>(g, (int)blockIdx.x, (int)blockIdx.y, (int)blockIdx.z);
 }
 
+// Several GEMMs of one rate, codebook and row-block count in one launch (a group of linears
+// over the same rows, engine/exl3/exl3.h:328-389 runs them as one LinPolicyKernel): job j
+// owns workgroups [start[j], start[j + 1]), laid out as its own launch's (gx[j], entries)
+// grid, x fastest.  Each workgroup runs the same body as that launch, so the outputs are
+// bitwise those of one launch per job.
+constexpr int kMaxMultiJobs = 12;  // the table stays within the 4 KB of kernel arguments
+struct GemmMulti {
+  int n;
+  int start[kMaxMultiJobs + 1];
+  int gx[kMaxMultiJobs];
+  GemmArgs g[kMaxMultiJobs];
+};
+template <int K2, int CB, int NRB, int KSW, int U>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NRB == 1 && K2 <= 8 ? 8 : 1)))
+Exl3GemmMultiKernel(GemmMulti gm) {
+  const int L = (int)blockIdx.x;
+  int j = 0;
+  while (j + 1 < gm.n && L >= gm.start[j + 1]) ++j;  // uniform
+  const int loc = L - gm.start[j];
+  GemmBody<K2, CB, NRB, KSW, U, false, 0>(gm.g[j], loc % gm.gx[j], loc / gm.gx[j], 0);
+}
+
 // Decode calls: the gate/up GEMM, the mid and the down GEMM (output transform in its
 // epilogue) in one launch, with no fence and no data leaving an XCD.  Workgroups go to the
 // 8 XCDs round-robin by linear id; workgroup L serves row entry e with e % 8 = L % 8, so

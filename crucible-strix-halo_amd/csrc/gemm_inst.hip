@@ -52,6 +52,31 @@ bool CX_CAT(LaunchGemmRate, CX_RATE)(int cb, int nrb, int ksw, dim3 grid, const 
   return false;
 }
 
+bool CX_CAT(LaunchGemmMultiRate, CX_RATE)(int cb, int nrb, const GemmMulti& gm, hipStream_t s) {
+  constexpr int K2 = CX_RATE;
+  constexpr int U = 2;
+  auto go = [&](auto cbc, auto nrbc) {
+    constexpr int CB = decltype(cbc)::value, NRB = decltype(nrbc)::value;
+    hipLaunchKernelGGL((Exl3GemmMultiKernel<K2, CB, NRB, 4, U>), dim3((unsigned)gm.start[gm.n]), dim3(256), 0, s, gm);
+    return true;
+  };
+  auto rows = [&](auto cbc) {
+    switch (nrb) {
+      case 1: return go(cbc, IC<1>{});
+      case 2: return go(cbc, IC<2>{});
+      case 3: return go(cbc, IC<3>{});
+      case 4: return go(cbc, IC<4>{});
+      default: return false;
+    }
+  };
+  if (cb == kCbMul1) return rows(IC<kCbMul1>{});
+  if constexpr (K2 % 2 == 0) {
+    if (cb == kCbMcg) return rows(IC<kCbMcg>{});
+    if (cb == kCb3Inst) return rows(IC<kCb3Inst>{});
+  }
+  return false;
+}
+
 bool CX_CAT(LaunchDecodeStageRate, CX_RATE)(int cb, const GemmArgs& gu, const GemmArgs& dn, int nyp, hipStream_t s) {
   constexpr int K2 = CX_RATE;
   const unsigned blocks = (unsigned)((2 * gu.ncp + dn.ncp / 4) * nyp);

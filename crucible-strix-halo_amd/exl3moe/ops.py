@@ -97,6 +97,15 @@ class DeviceLinear:
         return y
 
 
+def group_workspace_size(lins, M: int) -> int:
+    """Workspace bytes of cx_exl3_group for these DeviceLinears over M rows."""
+    from . import Job
+    arr = (Job * len(lins))()
+    for i, lin in enumerate(lins):
+        arr[i] = Job(lin.struct, None, CX_F16, lin.in_features, None, CX_F32, lin.out_features)
+    return int(lib().cx_exl3_group_workspace_size(arr, len(lins), M))
+
+
 def linear_group(jobs, row_offsets=None, workspace=None, stream=None):
     """Runs EXL3 linears over the same rows in one group (cx_exl3_group).  jobs: list of
     (DeviceLinear, x [M][>= I] fp16/fp32, y [M][>= O] fp16/fp32), rows contiguous in the

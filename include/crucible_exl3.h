@@ -138,9 +138,10 @@ typedef struct cx_moe_expert {
 
 /* A group of EXL3 linears applied to the same M rows, each with its own input and output
  * (e.g. the attention projections or the expert matrices of one decode step): one input-
- * transform launch for all jobs, one decode-GEMM launch per job, one output-transform
- * launch for all jobs.  Replaces Build + RunGroup over LinJobs (engine/engine.hip:
- * 1046-1106, 1731-1746; engine/exl3/exl3.h:20-41).  fp32 inputs are rounded to fp16
+ * transform launch for all jobs, one decode-GEMM launch per rate and codebook (up to 12
+ * jobs each), one output-transform launch for all jobs.  Replaces Build + RunGroup over
+ * LinJobs (engine/engine.hip:1046-1106, 1731-1746; engine/exl3/exl3.h:20-41, the group's
+ * LinPolicyKernel launch engine/exl3/exl3.h:328-389).  fp32 inputs are rounded to fp16
  * before the input transform, as the reference's fp32 sources are.
  *   x   [M][ldx] of x_dtype (CX_F16 / CX_F32), y [M][ldy] of y_dtype; ldx, ldy multiples of 8
  *   at most 16 jobs; workspace per cx_exl3_group_workspace_size */

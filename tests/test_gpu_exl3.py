@@ -228,6 +228,32 @@ def test_linear_group(ops):
         assert torch.all(y.as_strided((M, 8), (y.stride(0), 1), y.shape[1]) == 3.0)  # padding untouched
 
 
+def test_linear_group_one_launch_per_rate(ops):
+    # 13 jobs at 4 bpw (mul1) over the same ragged rows share GEMM launches (12 + 1 jobs),
+    # beside two 3-bpw jobs (one more launch) and an mcg job (a launch of its own): each
+    # job bitwise equal to its own cx_exl3_linear call and within tolerance of the oracle.
+    from exl3moe import synth
+    rng = np.random.default_rng(33)
+    specs = [(128 * int(rng.integers(1, 13)), 128 * int(rng.integers(1, 13)), 4, "mul1") for _ in range(13)]
+    specs += [(512, 640, 3, "mul1"), (1024, 256, 3, "mul1"), (256, 384, 4, "mcg")]
+    offs = [0, 2, 7, 8, 19]
+    M = offs[-1]
+    jobs, singles, refs = [], [], []
+    for I, Ot, bits, cb in specs:
+        tr, suh, svh = synth.linear(rng, I, Ot, bits)
+        lin = ops.DeviceLinear.from_trellis(tr, suh, svh, bits, codebook=cb)
+        x = torch.from_numpy(rng.standard_normal((M, I)).astype(np.float16)).cuda()
+        y = torch.empty(M, Ot, dtype=torch.float32, device="cuda")
+        jobs.append((lin, x, y))
+        singles.append(lin(x, torch.float32, row_offsets=offs).cpu().numpy())
+        refs.append(O.matvec(x.cpu().numpy(), O.reconstruct_inner(tr, bits, cb), suh, svh, np.float32))
+    ops.linear_group(jobs, row_offsets=offs)
+    for (lin, x, y), single, ref in zip(jobs, singles, refs):
+        got = y.cpu().numpy()
+        np.testing.assert_array_equal(got.view(np.uint32), single.view(np.uint32))
+        assert rel_l2(got, ref) <= 1e-3
+
+
 def test_linear_group_errors(ops):
     from exl3moe import Job, lib, synth
     import ctypes
