@@ -49,7 +49,7 @@ def oracle_layer(plan, x, sel, wts):
 
 def test_route_exact(ops):
     rng = np.random.default_rng(0)
-    for M, E, k in [(24, 512, 10), (2048, 512, 10), (5, 64, 8), (3, 1000, 16)]:
+    for M, E, k in [(24, 512, 10), (2048, 512, 10), (5, 64, 8), (3, 1000, 16), (7, 1024, 32), (300, 96, 32), (2, 16, 1)]:
         lg = rng.standard_normal((M, E + 1)).astype(np.float32)
         lg[0, 7] = lg[0, 300 % E] = lg[0, 9] = 5.0  # a three-way tie: lower ids first
         sel, wts = ops.route(torch.from_numpy(lg).cuda(), E, k)
