@@ -216,6 +216,25 @@ def test_uneven_block_counts(ops, E, H, Ie, k):
         assert np.abs(y - ref).max() <= 2e-3 * np.abs(ref).max()
 
 
+def test_largest_expert_count_and_topk(ops):
+    # E = 1024 experts (the library's maximum: 16 logits per routing lane) and top-32 (its
+    # maximum top-k, past the row-parallel limits of every kernel), decode (fused routing
+    # at <= 16 rows, separate above) and prefill, against the oracle.
+    from exl3moe import synth
+    plan = synth.device_moe_layer(77, E=1024, H=128, Ie=128, topk=32)
+    rng = np.random.default_rng(77)
+    for M, mode in ((3, 1), (20, 1), (150, 2)):
+        x = rng.standard_normal((M, 128)).astype(np.float16)
+        lg = rng.standard_normal((M, 1025)).astype(np.float32)
+        print(f"E=1024 k=32 M={M} mode={mode}", flush=True)
+        y, sel, wts = run_layer(plan, x, lg, mode)
+        rs, rw = O.route(lg, 1024, 32)
+        np.testing.assert_array_equal(sel, rs)
+        e = rel_l2(y, oracle_layer(plan, x, rs, rw))
+        print(f"  rel_l2={e:.3e}")
+        assert e <= 1e-3
+
+
 def test_tall_prefill_mixed_rates(ops):
     # The shared expert at other rates than the routed ones: each GEMM runs as two launches
     # (shared entries, then routed), and the tall gate/up launch computes the mid itself in
