@@ -208,19 +208,19 @@ bool LaunchGemmPrefill(int k2, int cb, int nrbt, int wpg, bool mid, dim3 grid, c
   }
 }
 
-bool LaunchDecodeStage(int k2, int cb, const GemmArgs& gu, const GemmArgs& dn, int nyp, hipStream_t s) {
+bool LaunchDecodeStage(int k2, int k2d, int cb, const GemmArgs& gu, const GemmArgs& dn, int nyp, hipStream_t s) {
   switch (k2) {
-    case 2: return LaunchDecodeStageRate2(cb, gu, dn, nyp, s);
-    case 3: return LaunchDecodeStageRate3(cb, gu, dn, nyp, s);
-    case 4: return LaunchDecodeStageRate4(cb, gu, dn, nyp, s);
-    case 5: return LaunchDecodeStageRate5(cb, gu, dn, nyp, s);
-    case 6: return LaunchDecodeStageRate6(cb, gu, dn, nyp, s);
-    case 7: return LaunchDecodeStageRate7(cb, gu, dn, nyp, s);
-    case 8: return LaunchDecodeStageRate8(cb, gu, dn, nyp, s);
-    case 10: return LaunchDecodeStageRate10(cb, gu, dn, nyp, s);
-    case 12: return LaunchDecodeStageRate12(cb, gu, dn, nyp, s);
-    case 14: return LaunchDecodeStageRate14(cb, gu, dn, nyp, s);
-    case 16: return LaunchDecodeStageRate16(cb, gu, dn, nyp, s);
+    case 2: return LaunchDecodeStageRate2(cb, k2d, gu, dn, nyp, s);
+    case 3: return LaunchDecodeStageRate3(cb, k2d, gu, dn, nyp, s);
+    case 4: return LaunchDecodeStageRate4(cb, k2d, gu, dn, nyp, s);
+    case 5: return LaunchDecodeStageRate5(cb, k2d, gu, dn, nyp, s);
+    case 6: return LaunchDecodeStageRate6(cb, k2d, gu, dn, nyp, s);
+    case 7: return LaunchDecodeStageRate7(cb, k2d, gu, dn, nyp, s);
+    case 8: return LaunchDecodeStageRate8(cb, k2d, gu, dn, nyp, s);
+    case 10: return LaunchDecodeStageRate10(cb, k2d, gu, dn, nyp, s);
+    case 12: return LaunchDecodeStageRate12(cb, k2d, gu, dn, nyp, s);
+    case 14: return LaunchDecodeStageRate14(cb, k2d, gu, dn, nyp, s);
+    case 16: return LaunchDecodeStageRate16(cb, k2d, gu, dn, nyp, s);
     default: return false;
   }
 }

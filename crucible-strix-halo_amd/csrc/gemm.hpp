@@ -617,9 +617,9 @@ Exl3GemmMultiKernel(GemmMulti gm) {
 // the down workgroups.  Every gate/up workgroup precedes every down workgroup in dispatch
 // order, and only down workgroups wait, so every wait ends.  nyp: the entry table's
 // length, a multiple of 8 (entries past the device-side count have 0 rows).  The counters
-// are zeroed by the grouping launch before.
-template <int K2, int CB>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(K2 <= 8 ? 8 : 1)))
+// are zeroed by the grouping launch before.  K2: the gate/up rate, K2D the down rate.
+template <int K2, int K2D, int CB>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(K2 <= 8 && K2D <= 8 ? 8 : 1)))
 Exl3DecodeStageKernel(GemmArgs gu, GemmArgs dn, int nyp) {
   const int L = (int)blockIdx.x, x = L & 7;
   const int n = (min(*gu.n_entries, nyp) + 7) & ~7;
@@ -629,7 +629,7 @@ Exl3DecodeStageKernel(GemmArgs gu, GemmArgs dn, int nyp) {
     GemmBody<K2, CB, 1, 4, 2, false, 1>(gu, j % gu.ncp, e, j / gu.ncp);
   } else if (L < n_gu + per_dn * n) {
     const int k = (L - n_gu) >> 3, e = 8 * (k / per_dn) + x, j = k % per_dn;
-    GemmBody<K2, CB, 1, 1, 2, false, 2>(dn, j, e, 0);
+    GemmBody<K2D, CB, 1, 1, 2, false, 2>(dn, j, e, 0);
   }
 }
 

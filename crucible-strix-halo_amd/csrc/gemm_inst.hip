@@ -77,14 +77,32 @@ bool CX_CAT(LaunchGemmMultiRate, CX_RATE)(int cb, int nrb, const GemmMulti& gm, 
   return false;
 }
 
-bool CX_CAT(LaunchDecodeStageRate, CX_RATE)(int cb, const GemmArgs& gu, const GemmArgs& dn, int nyp, hipStream_t s) {
+// The down rates a stage launch of gate/up rate K2 takes: K2 itself (every codebook), and
+// for mul1 layers the next two rates up (K2 + 2, K2 + 4: e.g. 3 bpw gate/up with 4 or 5 bpw
+// down).
+constexpr bool StageDownRate(int k2d) { return (k2d >= 2 && k2d <= 16 && k2d % 2 == 0) || k2d == 3 || k2d == 5 || k2d == 7; }
+
+bool CX_CAT(LaunchDecodeStageRate, CX_RATE)(int cb, int k2d, const GemmArgs& gu, const GemmArgs& dn, int nyp,
+                                             hipStream_t s) {
   constexpr int K2 = CX_RATE;
   const unsigned blocks = (unsigned)((2 * gu.ncp + dn.ncp / 4) * nyp);
   auto go = [&](auto cbc) {
     constexpr int CB = decltype(cbc)::value;
-    hipLaunchKernelGGL((Exl3DecodeStageKernel<K2, CB>), dim3(blocks), dim3(256), 0, s, gu, dn, nyp);
+    hipLaunchKernelGGL((Exl3DecodeStageKernel<K2, K2, CB>), dim3(blocks), dim3(256), 0, s, gu, dn, nyp);
     return true;
   };
+  auto mixed = [&](auto k2dc) {
+    constexpr int K2D = decltype(k2dc)::value;
+    if constexpr (StageDownRate(K2D))
+      hipLaunchKernelGGL((Exl3DecodeStageKernel<K2, K2D, kCbMul1>), dim3(blocks), dim3(256), 0, s, gu, dn, nyp);
+    return StageDownRate(K2D);
+  };
+  if (k2d != K2) {
+    if (cb != kCbMul1) return false;
+    if (k2d == K2 + 2) return mixed(IC<K2 + 2>{});
+    if (k2d == K2 + 4) return mixed(IC<K2 + 4>{});
+    return false;
+  }
   if (cb == kCbMul1) return go(IC<kCbMul1>{});
   if constexpr (K2 % 2 == 0) {
     if (cb == kCbMcg) return go(IC<kCbMcg>{});

@@ -102,7 +102,7 @@ constexpr int kTallRowBlocksPerWave = 3;
 bool LaunchGemmTall(int k2, int cb, dim3 grid, const GemmArgs& g, hipStream_t s);
 // Gate/up, mid and down of a decode call in one launch (Exl3DecodeStageKernel), all four
 // matrices of every expert at rate k2 and codebook cb; nyp entries (a multiple of 8).
-bool LaunchDecodeStage(int k2, int cb, const GemmArgs& gu, const GemmArgs& dn, int nyp, hipStream_t s);
+bool LaunchDecodeStage(int k2, int k2d, int cb, const GemmArgs& gu, const GemmArgs& dn, int nyp, hipStream_t s);
 // Exl3GemmMultiKernel: gm.n jobs (K split over 4 waves) at rate k2, codebook cb, nrb row
 // blocks; gm.start[gm.n] workgroups.
 bool LaunchGemmMulti(int k2, int cb, int nrb, const GemmMulti& gm, hipStream_t s);
@@ -112,7 +112,7 @@ bool LaunchGemmMulti(int k2, int cb, int nrb, const GemmMulti& gm, hipStream_t s
   bool LaunchGemmPrefillRate##K2(int cb, int nrbt, int wpg, bool mid, dim3 grid, const GemmArgs& g, \
                                  hipStream_t s);                                                         \
   bool LaunchGemmTallRate##K2(int cb, dim3 grid, const GemmArgs& g, hipStream_t s);                         \
-  bool LaunchDecodeStageRate##K2(int cb, const GemmArgs& gu, const GemmArgs& dn, int nyp, hipStream_t s); \
+  bool LaunchDecodeStageRate##K2(int cb, int k2d, const GemmArgs& gu, const GemmArgs& dn, int nyp, hipStream_t s); \
   bool LaunchGemmMultiRate##K2(int cb, int nrb, const GemmMulti& gm, hipStream_t s);
 CX_DECLARE_RATE(2)
 CX_DECLARE_RATE(3)

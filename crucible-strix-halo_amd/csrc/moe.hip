@@ -774,15 +774,18 @@ MoeSizes PlanMoe(const cx_moe_plan* pl, int M, int mode) {
   // Switch CX_DOWN_MID = 0 / 1 forces it off / on (decode, I <= 1024).
   s.down_mid = decode && pl->I <= 1024 &&
                (ps.down_mid < 0 ? (long)M * (pl->topk + 1) <= 128 : ps.down_mid != 0);
-  // Decode calls through the grouping launch with every matrix at one rate and codebook,
+  // Decode calls through the grouping launch with one codebook and the stage launch's rates,
   // above the prologue mid's range: gate/up, the mid and down in one launch
   // (Exl3DecodeStageKernel).  Measured on config 3 (median per layer call, 200 calls):
   // 12 rows 74.8 -> 66.3 us, 16 rows 87.6 -> 80.4, 24 rows 111.7 -> 102.7, 32 rows
   // 128.8 -> 124, 64 rows 188.7 -> 181; at 1-8 rows, against the down GEMM with the
   // prologue mid, no change (29.4 / 58.5 us) or a little slower (R = 1 in bench: 31.6
   // against 30.8 us).
-  s.stage = decode && ps.stage != 0 && pl->xcd_rr && FrontEndFits(M, pl->E, pl->topk) && !s.down_mid && pl->k2_gu == pl->k2_d &&
-            pl->k2_gu == pl->k2_sgu && pl->k2_gu == pl->k2_sd && pl->cb_gu == pl->cb_d && pl->cb_gu == pl->cb_sgu &&
+  // The down rate may exceed the gate/up rate by one or two steps for mul1 layers (the
+  // launch's instantiations); the shared expert at the routed experts' rates.
+  const bool stage_rates = pl->k2_d == pl->k2_gu || (pl->cb_d == kCbMul1 && (pl->k2_d == pl->k2_gu + 2 || pl->k2_d == pl->k2_gu + 4));
+  s.stage = decode && ps.stage != 0 && pl->xcd_rr && FrontEndFits(M, pl->E, pl->topk) && !s.down_mid && stage_rates &&
+            pl->k2_gu == pl->k2_sgu && pl->k2_d == pl->k2_sd && pl->cb_gu == pl->cb_d && pl->cb_gu == pl->cb_sgu &&
             pl->cb_gu == pl->cb_sd && pl->I % 128 == 0;
   // Decode: one 16-row block per entry; prefill: every row of an entry shares each decoded tile.
   s.chunk = 16 * s.nrb;
@@ -1239,7 +1242,7 @@ int MoeForward(const cx_moe_plan* pl, const void* x, int32_t x_dtype, int32_t ld
     gu.n_entries = dn.n_entries = nent;
     gu.stage_ctr = dn.stage_ctr = ctr;
     gu.stage_arrivals = dn.stage_arrivals = 2 * gu.ncp;
-    if (!LaunchDecodeStage(pl->k2_gu, pl->cb_gu, gu, dn, sz.nyp, s)) return CX_E_UNSUPPORTED;
+    if (!LaunchDecodeStage(pl->k2_gu, pl->k2_d, pl->cb_gu, gu, dn, sz.nyp, s)) return CX_E_UNSUPPORTED;
     mark();
     mark();
   } else {

@@ -63,22 +63,26 @@ def test_switch(monkeypatch, env, cases):
         assert np.abs(y - ref).max() <= 2e-3 * np.abs(ref).max()
 
 
-@pytest.mark.parametrize("E,H,Ie,k,sizes", [(512, 2048, 512, 10, (1, 3, 8, 17, 24, 40, 64)),
-                                            (16, 256, 256, 4, (1, 5, 33, 64)), (3, 128, 128, 2, (50, 64))])
-def test_stage_launch_bitwise(monkeypatch, E, H, Ie, k, sizes):
+@pytest.mark.parametrize("E,H,Ie,k,sizes,bits", [(512, 2048, 512, 10, (1, 3, 8, 17, 24, 40, 64), (4, 4)),
+                                                 (16, 256, 256, 4, (1, 5, 33, 64), (4, 4)),
+                                                 (3, 128, 128, 2, (50, 64), (4, 4)),
+                                                 (512, 2048, 512, 10, (12, 24, 40), (3, 5)),
+                                                 (16, 256, 256, 4, (33, 64), (4, 5))])
+def test_stage_launch_bitwise(monkeypatch, E, H, Ie, k, sizes, bits):
     """Decode calls with gate/up, mid and down in one launch (the default) against the same
     calls in separate launches: the same GEMM bodies and mid arithmetic, so the outputs,
     selections and weights are bitwise equal; a layer with fewer than 8 routed experts
-    leaves some XCDs without entries."""
+    leaves some XCDs without entries; down rates above the gate/up rate (3 / 5 and 4 / 5 bits
+    per weight) take the mixed-rate instantiations."""
     if not torch.cuda.is_available():
         pytest.skip("no GPU")
     from exl3moe import synth
     for key in ALL:
         monkeypatch.delenv(key, raising=False)
     monkeypatch.setenv("CX_STAGE", "0")
-    sep = synth.device_moe_layer(500 + E, E=E, H=H, Ie=Ie, topk=k)
+    sep = synth.device_moe_layer(500 + E, E=E, H=H, Ie=Ie, topk=k, bits_gu=bits[0], bits_d=bits[1])
     monkeypatch.delenv("CX_STAGE")
-    one = synth.device_moe_layer(500 + E, E=E, H=H, Ie=Ie, topk=k)
+    one = synth.device_moe_layer(500 + E, E=E, H=H, Ie=Ie, topk=k, bits_gu=bits[0], bits_d=bits[1])
     rng = np.random.default_rng(E)
     for M in sizes:
         print(f"stage launch E={E} M={M}", flush=True)
