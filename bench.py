@@ -33,7 +33,7 @@ MFMA_F16_PEAK_TFS = 2500.0  # MI355X dense fp16 MFMA, published (no sparsity)
 E, H, IE, TOPK = 512, 2048, 512, 10
 
 
-STAGE_KERNEL = "Exl3DecodeStageKernel<8, 2>"  # gate/up + mid + down of a decode call in one launch (4.0 bpw, mul1)
+STAGE_KERNEL = "Exl3DecodeStageKernel<8, 8, 2>"  # gate/up + mid + down of a decode call in one launch (4.0 bpw, mul1)
 
 
 def uses_stage(M):
